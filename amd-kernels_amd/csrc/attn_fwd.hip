@@ -1,0 +1,590 @@
+// bf16 flash-attention forward for MI355X (gfx950), head_dim 128, no mask.
+//
+//   O = softmax(Q K^T / sqrt(128)) V,  bf16 in / bf16 out, fp32 accumulate.
+//
+// Replaces the reference's gfx942 kernel family (moonmath reference
+// csrc/attention_kernel.hip:454-1127 forward, :1137-1217 V transpose,
+// :1221-1279 merge, :1286-1393 tail planner) with a gfx950-native design:
+//
+//  * MFMA v_mfma_f32_32x32x16_bf16. Scores are computed transposed,
+//    S^T = K Q^T (A = K fragment, B = Q fragment), so each lane owns one query
+//    column and 16 kv rows per 32x32 tile; P^T then feeds O^T = V^T P^T as the
+//    B operand straight from registers (no shuffle).
+//  * K and the pre-transposed V_t are staged through LDS with 16-byte
+//    global->LDS DMA (global_load_lds_dwordx4), double buffered. K is stored
+//    in MFMA fragment order so every operand read is a conflict-free
+//    ds_read_b128 at base + 16*lane.
+//  * Online softmax in base 2 with the running max kept on the integer grid:
+//    m = ceil(max(s) * log2(e)/sqrt(128)). Every rescale is an exact power of
+//    two, so the bf16 rounding of P (done with the output round mode, as in
+//    the reference :438-449) does not depend on the KV blocking, on the
+//    KV-split factor or on the merge order. The denominator sums unrounded
+//    fp32 p (reference :445-451).
+//  * Output: (O * rcp(l)) rounded per mode with every NaN -> 0x7FFF; l == 0
+//    gives inv = 0 (reference :1114-1117).
+//  * KV split: the CTAs of the last, partially filled round of the grid
+//    (the "tail") can be split over KV into G contiguous block ranges; each
+//    part writes unnormalised fp32 (O, m, l) and a merge kernel combines them
+//    (reference :1094-1112, :1239-1279).
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mm_common.hpp"
+
+namespace mm {
+namespace attn {
+
+constexpr int kD = 128;            // head_dim
+constexpr int kKvBlock = 64;       // kv rows per main-loop block
+constexpr int kWaves = 4;          // waves per CTA
+constexpr int kThreads = 64 * kWaves;
+constexpr int kQRowsPerTile = 32;  // q rows per 32x32 MFMA tile
+constexpr int kFragBytes = 1024;   // one 32x16 bf16 MFMA operand fragment (64 lanes x 16 B)
+constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
+constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
+constexpr int kStageBytes = kKBytes + kVBytes;
+constexpr int kVtBlockElems = kKvBlock * kD; // 8192 bf16 per V_t block
+
+// Split-KV limits: partial records are laid out for CTAs of up to kMaxRows q
+// rows and kMaxParts parts.
+constexpr int kMaxRows = 256;
+constexpr int kMaxParts = 1024;
+constexpr size_t kPartOFloats = (size_t)kMaxRows * kD;
+constexpr size_t kWorkspaceBytes = (size_t)kMaxParts * kMaxRows * (kD + 2) * sizeof(float);
+
+struct Params {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* vt;
+  uint16_t* out;
+  float* ws;         // split partials (null unless split)
+  int B, H, Sq, Skv;
+  int bshd;          // 1 = [B,S,H,D], 0 = [B,H,S,D]
+  int nqb, nkb;      // q-blocks per head, kv blocks per head
+  int prefix_wgs;    // CTAs that run the whole KV stream
+  int split_ways;    // G (parts per tail q-block)
+  float scale_log2e; // log2(e) / sqrt(128), rounded to fp32 on the host
+};
+
+// Element offset of (b, h, s=0, d=0) and the stride between seq positions.
+__device__ __forceinline__ long long head_base(int b, int h, int S, int H, int bshd) {
+  return bshd ? ((long long)b * S * H + h) * kD : ((long long)b * H + h) * (long long)S * kD;
+}
+
+template <int MODE, int QT>
+__device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb_begin, int kb_end, int part,
+                                         char* lds) {
+  constexpr int kRows = kWaves * QT * kQRowsPerTile;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r = lane & 31;  // query column owned by this lane in every tile
+  const int g = lane >> 5;  // lane half
+
+  const int b = bh / p.H, h = bh % p.H;
+  const long long row_stride = p.bshd ? (long long)p.H * kD : kD;
+  const uint16_t* qh = p.q + head_base(b, h, p.Sq, p.H, p.bshd);
+  const uint16_t* kh = p.k + head_base(b, h, p.Skv, p.H, p.bshd);
+  const uint16_t* vth = p.vt + (long long)bh * p.nkb * kVtBlockElems;
+  const float c = p.scale_log2e;
+
+  // ---- K / V_t DMA for one kv block into one LDS stage ----------------------
+  // Stage layout: K fragments [t(2)][ds(8)] then V_t fragments [t(2)][s(2)][dt(4)],
+  // each 1 KB in lane order. Wave w moves fragments 4w..4w+3 of each.
+  auto issue_block = [&](int kb, int stage) {
+    char* st = lds + stage * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = wave * 4 + i;
+      const int t = f >> 3, ds = f & 7;
+      int kv = kb * kKvBlock + t * 32 + r;
+      kv = kv < p.Skv ? kv : p.Skv - 1;  // rows past Skv are masked in softmax
+      const uint16_t* src = kh + (long long)kv * row_stride + ds * 16 + g * 8;
+      dma16(src, (MM_LDS void*)(st + f * kFragBytes));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = wave * 4 + i;
+      const uint16_t* src = vth + (long long)kb * kVtBlockElems + f * 512 + lane * 8;
+      dma16(src, (MM_LDS void*)(st + kKBytes + f * kFragBytes));
+    }
+  };
+
+  // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
+  bf16x8 qf[QT][8];
+  const int q_row0 = qb * kRows + wave * QT * kQRowsPerTile;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    int qr = q_row0 + qt * kQRowsPerTile + r;
+    qr = qr < p.Sq ? qr : p.Sq - 1;
+    const uint16_t* src = qh + (long long)qr * row_stride + g * 8;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) qf[qt][ds] = *reinterpret_cast<const bf16x8*>(src + ds * 16);
+  }
+
+  f32x16 oacc[QT][4];
+  float row_m[QT], row_l[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    row_m[qt] = kNegFltMax;
+    row_l[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] = f32x16{};
+  }
+
+  if (kb_begin < kb_end) issue_block(kb_begin, 0);
+
+  for (int kb = kb_begin; kb < kb_end; ++kb) {
+    const int stage = (kb - kb_begin) & 1;
+    if (kb + 1 < kb_end) {
+      issue_block(kb + 1, stage ^ 1);
+      wait_vmem_barrier<8>();
+    } else {
+      wait_vmem_barrier<0>();
+    }
+    const char* kst = lds + stage * kStageBytes;
+    const char* vst = kst + kKBytes;
+
+    // ---- S^T = K Q^T ---------------------------------------------------------
+    f32x16 sacc[2][QT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) sacc[t][qt] = f32x16{};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + (t * 8 + ds) * kFragBytes + lane * 16);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) sacc[t][qt] = mfma32(kf, qf[qt][ds], sacc[t][qt]);
+      }
+    }
+
+    // ---- mask kv rows past Skv (last block only) ------------------------------
+    const int kv0 = kb * kKvBlock;
+    if (kv0 + kKvBlock > p.Skv) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = kv0 + t * 32 + (i >> 2) * 8 + g * 4 + (i & 3);
+          if (kv >= p.Skv) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) sacc[t][qt][i] = -__builtin_inff();
+          }
+        }
+    }
+
+    // ---- online softmax (integer-grid running max) ----------------------------
+    bf16x8 pf[QT][2][2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float bm = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) bm = fmaxf(bm, sacc[t][qt][i]);
+      bm = xor32_max(bm);
+      const float mb = __builtin_ceilf(bm * c);
+      const float m_old = row_m[qt];
+      const float m_new = fmaxf(m_old, mb);
+      const bool grew = m_new > m_old;
+      if (__builtin_amdgcn_ballot_w64(grew)) {
+        const float diff = m_old - m_new;  // integer-valued, <= 0 when grew
+        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
+        sc = (diff >= -126.f) ? sc : 0.f;
+        sc = grew ? sc : 1.f;
+        row_l[qt] *= sc;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= sc;
+      }
+      row_m[qt] = m_new;
+      const float neg_m = -m_new;
+      float lsum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          uint32_t w[4];
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][qt][8 * s + 2 * e2], c, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][qt][8 * s + 2 * e2 + 1], c, neg_m));
+            lsum += p0;
+            lsum += p1;
+            w[e2] = pack2_bf16<MODE>(p0, p1);
+          }
+          u32x4 wv = {w[0], w[1], w[2], w[3]};
+          pf[qt][t][s] = __builtin_bit_cast(bf16x8, wv);
+        }
+      }
+      row_l[qt] += lsum;
+    }
+
+    // ---- O^T += V^T P^T ---------------------------------------------------------
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const bf16x8 vf =
+              *reinterpret_cast<const bf16x8*>(vst + ((t * 2 + s) * 4 + dt) * kFragBytes + lane * 16);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) oacc[qt][dt] = mfma32(vf, pf[qt][t][s], oacc[qt][dt]);
+        }
+      }
+    }
+    lds_reads_done_barrier();
+  }
+
+  // ---- epilogue -----------------------------------------------------------------
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) row_l[qt] = xor32_sum(row_l[qt]);
+
+  if (part >= 0) {
+    // Split part: unnormalised fp32 partials. Record layout per part:
+    // O [kMaxRows][128] fp32 then (m, l) [kMaxRows][2] fp32.
+    float* po = p.ws + (size_t)part * kPartOFloats;
+    float* pml = p.ws + (size_t)kMaxParts * kPartOFloats + (size_t)part * kMaxRows * 2;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int row = (wave * QT + qt) * kQRowsPerTile + r;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = dt * 32 + j * 8 + g * 4;
+          f32x4 v = {oacc[qt][dt][4 * j], oacc[qt][dt][4 * j + 1], oacc[qt][dt][4 * j + 2], oacc[qt][dt][4 * j + 3]};
+          *reinterpret_cast<f32x4*>(po + (size_t)row * kD + d) = v;
+        }
+      if (g == 0) {
+        pml[row * 2] = row_m[qt];
+        pml[row * 2 + 1] = row_l[qt];
+      }
+    }
+    return;
+  }
+
+  uint16_t* oh = p.out + head_base(b, h, p.Sq, p.H, p.bshd);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qr = q_row0 + qt * kQRowsPerTile + r;
+    if (qr >= p.Sq) continue;
+    const float l = row_l[qt];
+    const float inv = (l == 0.f) ? 0.f : __builtin_amdgcn_rcpf(l);
+    uint16_t* orow = oh + (long long)qr * row_stride;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = dt * 32 + j * 8 + g * 4;
+        u32x2 w;
+        w[0] = pack2_bf16_canon<MODE>(oacc[qt][dt][4 * j] * inv, oacc[qt][dt][4 * j + 1] * inv);
+        w[1] = pack2_bf16_canon<MODE>(oacc[qt][dt][4 * j + 2] * inv, oacc[qt][dt][4 * j + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+  }
+}
+
+template <int MODE, int QT, int MINB>
+__global__ __launch_bounds__(kThreads, MINB) void attn_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStageBytes];
+  const int idx = blockIdx.x;
+  if (idx < p.prefix_wgs) {
+    const int w = xcd_remap(idx, p.prefix_wgs);
+    run_tile<MODE, QT>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
+  } else {
+    // Split part: tail q-block t, part j of G, contiguous kv-block range.
+    const int part = idx - p.prefix_wgs;
+    const int t = part / p.split_ways, j = part % p.split_ways;
+    const int w = p.prefix_wgs + t;
+    const int kb0 = (int)((long long)p.nkb * j / p.split_ways);
+    const int kb1 = (int)((long long)p.nkb * (j + 1) / p.split_ways);
+    run_tile<MODE, QT>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Merge of split partials. One thread = 4 consecutive d of one row.
+// M = max_p m_p; w_p = 2^(m_p - M) (exact, m_p integer-valued);
+// out = mode(sum_p w_p O_p * rcp(sum_p w_p l_p)), inv = 0 when the sum is 0.
+// ---------------------------------------------------------------------------
+constexpr int kMergeThreads = 256;
+
+__device__ __forceinline__ float pow2_weight(float m_p, float M) {
+  if (m_p == M) return 1.f;  // also covers M == +inf with m_p == +inf
+  const float diff = m_p - M;  // < 0
+  const float w = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
+  return diff >= -126.f ? w : 0.f;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(Params p, int rows) {
+  const int per_qb = rows * kD / 4 / kMergeThreads;
+  const int t = blockIdx.x / per_qb;
+  const int cell = ((blockIdx.x % per_qb) * kMergeThreads + threadIdx.x) * 4;
+  const int row = cell / kD, d = cell % kD;
+  const int w = p.prefix_wgs + t;
+  const int bh = w / p.nqb, qb = w % p.nqb;
+  const int qr = qb * rows + row;
+  if (qr >= p.Sq) return;
+  const int G = p.split_ways;
+  const int part0 = t * G;
+  const float* pml = p.ws + (size_t)kMaxParts * kPartOFloats;
+  float M = kNegFltMax;
+  for (int j = 0; j < G; ++j) M = fmaxf(M, pml[(size_t)(part0 + j) * kMaxRows * 2 + row * 2]);
+  float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f, L = 0.f;
+  for (int j = 0; j < G; ++j) {
+    const float m_p = pml[(size_t)(part0 + j) * kMaxRows * 2 + row * 2];
+    const float l_p = pml[(size_t)(part0 + j) * kMaxRows * 2 + row * 2 + 1];
+    const f32x4 o = *reinterpret_cast<const f32x4*>(p.ws + (size_t)(part0 + j) * kPartOFloats + (size_t)row * kD + d);
+    const float wt = pow2_weight(m_p, M);
+    o0 = __builtin_fmaf(wt, o[0], o0);
+    o1 = __builtin_fmaf(wt, o[1], o1);
+    o2 = __builtin_fmaf(wt, o[2], o2);
+    o3 = __builtin_fmaf(wt, o[3], o3);
+    L = __builtin_fmaf(wt, l_p, L);
+  }
+  const float inv = (L == 0.f) ? 0.f : __builtin_amdgcn_rcpf(L);
+  const int b = bh / p.H, h = bh % p.H;
+  const long long row_stride = p.bshd ? (long long)p.H * kD : kD;
+  uint16_t* dst = p.out + head_base(b, h, p.Sq, p.H, p.bshd) + (long long)qr * row_stride + d;
+  u32x2 wv;
+  wv[0] = pack2_bf16_canon<MODE>(o0 * inv, o1 * inv);
+  wv[1] = pack2_bf16_canon<MODE>(o2 * inv, o3 * inv);
+  *reinterpret_cast<u32x2*>(dst) = wv;
+}
+
+// ---------------------------------------------------------------------------
+// V -> V_t: per (b, h, 64-row kv block), 16 fragments of 64 lanes x 8 bf16:
+//   V_t[bh][kb][(t*2+s)*4+dt][lane][e] = V[kb*64 + 32t + 16s + 8(e/4) + 4(lane/32) + e%4][32dt + lane%32]
+// which is the A-operand order of O^T = V^T P^T. Rows >= Skv are zero.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
+                                                          int H, int Skv, int nkb, int bshd) {
+  __shared__ uint16_t tile[kKvBlock][kD + 2];
+  const int kb = blockIdx.x % nkb;
+  const int bh = blockIdx.x / nkb;
+  const int b = bh / H, h = bh % H;
+  const long long row_stride = bshd ? (long long)H * kD : kD;
+  const uint16_t* vh = v + head_base(b, h, Skv, H, bshd);
+  const int tid = threadIdx.x;
+  // Load 64 rows x 256 B: 1024 16-byte pieces, 4 per thread.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int piece = tid + i * 256;
+    const int row = piece >> 4, col = (piece & 15) * 8;
+    const int kv = kb * kKvBlock + row;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (kv < Skv) val = *reinterpret_cast<const u32x4*>(vh + (long long)kv * row_stride + col);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[row][col + 2 * e] = (uint16_t)(val[e] & 0xFFFFu);
+      tile[row][col + 2 * e + 1] = (uint16_t)(val[e] >> 16);
+    }
+  }
+  __syncthreads();
+  uint16_t* dst = vt + ((long long)bh * nkb + kb) * kVtBlockElems;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int unit = tid + i * 256;  // (fragment, lane)
+    const int f = unit >> 6, lane = unit & 63;
+    const int t = f >> 3, s = (f >> 2) & 1, dt = f & 3;
+    const int gg = lane >> 5, d = dt * 32 + (lane & 31);
+    u32x4 out;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) {
+      const int ea = 2 * e2, eb = 2 * e2 + 1;
+      const int kva = t * 32 + s * 16 + (ea >> 2) * 8 + gg * 4 + (ea & 3);
+      const int kvb = t * 32 + s * 16 + (eb >> 2) * 8 + gg * 4 + (eb & 3);
+      out[e2] = (uint32_t)tile[kva][d] | ((uint32_t)tile[kvb][d] << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + (size_t)unit * 8) = out;
+  }
+}
+
+}  // namespace attn
+}  // namespace mm
+
+// ===========================================================================
+// Host side: planner + C ABI
+// ===========================================================================
+namespace {
+using namespace mm::attn;
+
+constexpr int kNumCUs = 256;
+// Kernel variant used by the launchers: QT q-tiles of 32 rows per wave and
+// MINB CTAs resident per CU.
+constexpr int kQT = 1;
+constexpr int kMinBlocks = 2;
+constexpr int kRowsPerCta = kWaves * kQT * kQRowsPerTile;
+constexpr int kSlots = kNumCUs * kMinBlocks;
+
+// Tail KV-split cost model (re-derived from reference
+// csrc/attention_kernel.hip:1349-1393 for 256 CUs and kMinBlocks CTAs per CU).
+constexpr int kMinKvBlocksToSplit = 48;
+constexpr int kMinBlocksPerPart = 4;
+constexpr int kMergeCostBlocks = 3;
+
+struct TailPlan {
+  int prefix_wgs, tail, split_ways, parts;
+};
+
+TailPlan plan_tail(int nqb, int nbh, int nkb, int slots, bool enable, int force_ways) {
+  const int wgs = nqb * nbh;
+  const TailPlan none{wgs, 0, 1, 0};
+  if (!enable) return none;
+  int tail = wgs % slots;
+  if (force_ways > 1) {
+    // Test hook: split the last `tail` CTAs (the whole grid if it tiles evenly).
+    if (tail == 0) tail = wgs < slots ? wgs : slots;
+    int G = force_ways;
+    if (G > nkb) G = nkb;
+    while (tail * G > kMaxParts) --G;
+    if (G < 2) return none;
+    return TailPlan{wgs - tail, tail, G, tail * G};
+  }
+  if (tail == 0 || tail > slots * 19 / 20 || nkb < kMinKvBlocksToSplit) return none;
+  int G = 1;
+  long long best = (long long)nkb + kMergeCostBlocks;
+  for (int gw = 2; gw <= kMaxParts / tail && nkb / gw >= kMinBlocksPerPart; ++gw) {
+    const long long rounds = ((long long)tail * gw + slots - 1) / slots;
+    const long long per_part = (nkb + gw - 1) / gw;
+    const long long span = rounds * per_part + kMergeCostBlocks;
+    if (span < best) {
+      best = span;
+      G = gw;
+    }
+  }
+  if (G == 1) return none;
+  return TailPlan{wgs - tail, tail, G, tail * G};
+}
+
+template <int MODE>
+int launch_fwd(const void* q, const void* k, const void* v_t, void* out, int batch, int heads, int seq_len,
+               int seq_len_kv, int head_dim, int layout, void* workspace, int force_ways, void* stream) {
+  if (batch <= 0 || heads <= 0) return 1;
+  if (seq_len <= 0) return 2;
+  if (head_dim != kD) return 3;
+  if (seq_len_kv <= 0) return 5;
+  if (layout != 0 && layout != 1) return 7;
+  if (!q || !k || !v_t || !out) return 8;
+  Params p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.vt = static_cast<const uint16_t*>(v_t);
+  p.out = static_cast<uint16_t*>(out);
+  p.ws = static_cast<float*>(workspace);
+  p.B = batch;
+  p.H = heads;
+  p.Sq = seq_len;
+  p.Skv = seq_len_kv;
+  p.bshd = layout;
+  p.nqb = (seq_len + kRowsPerCta - 1) / kRowsPerCta;
+  p.nkb = (seq_len_kv + kKvBlock - 1) / kKvBlock;
+  p.scale_log2e = (float)(1.4426950408889634 / 11.313708498984761);
+  const long long nbh = (long long)batch * heads;
+  if ((long long)p.nqb * nbh > 0x7FFFFFFFLL) return 9;
+  const TailPlan tp = plan_tail(p.nqb, (int)nbh, p.nkb, kSlots, workspace != nullptr, force_ways);
+  p.prefix_wgs = tp.prefix_wgs;
+  p.split_ways = tp.split_ways;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = tp.prefix_wgs + tp.parts;
+  hipLaunchKernelGGL((attn_fwd_kernel<MODE, kQT, kMinBlocks>), dim3(grid), dim3(kThreads), 0, st, p);
+  if (tp.parts > 0) {
+    const int per_qb = kRowsPerCta * kD / 4 / kMergeThreads;
+    hipLaunchKernelGGL((attn_merge_kernel<MODE>), dim3(tp.tail * per_qb), dim3(kMergeThreads), 0, st, p,
+                       kRowsPerCta);
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+int launch_vt(const void* v, void* v_t, int n_rows, int seq_len_per_head, int heads, int layout, void* stream) {
+  if (heads <= 0 || seq_len_per_head <= 0 || n_rows <= 0) return 1;
+  if (n_rows % ((long long)heads * seq_len_per_head) != 0) return 2;
+  if (layout != 0 && layout != 1) return 7;
+  if (!v || !v_t) return 8;
+  const int batch = (int)(n_rows / ((long long)heads * seq_len_per_head));
+  const int nkb = (seq_len_per_head + kKvBlock - 1) / kKvBlock;
+  const long long grid = (long long)batch * heads * nkb;
+  if (grid > 0x7FFFFFFFLL) return 9;
+  hipLaunchKernelGGL(v_transpose_kernel, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(v_t), heads, seq_len_per_head, nkb,
+                     layout);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
+}  // namespace
+
+extern "C" {
+
+#define MM_ATTN_MODE_SYMBOLS(NAME, MODE)                                                                      \
+  int launch_v_transpose_##NAME(const void* v, void* v_t, int n_rows, int seq_len_per_head, int heads,       \
+                                int layout, void* stream) {                                                  \
+    return launch_vt(v, v_t, n_rows, seq_len_per_head, heads, layout, stream);                               \
+  }                                                                                                          \
+  int launch_attention_forward_##NAME(const void* q, const void* k, const void* v_t, void* out, int batch,   \
+                                      int heads, int seq_len, int seq_len_kv, int head_dim, int layout,      \
+                                      void* workspace, void* stream) {                                       \
+    return launch_fwd<MODE>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, layout, workspace, \
+                            0, stream);                                                                      \
+  }                                                                                                          \
+  size_t tail_workspace_bytes_##NAME(void) { return kWorkspaceBytes; }
+
+MM_ATTN_MODE_SYMBOLS(rtne, mm::kRTNE)
+MM_ATTN_MODE_SYMBOLS(rtna, mm::kRTNA)
+MM_ATTN_MODE_SYMBOLS(rtz, mm::kRTZ)
+
+int moonmath_attention_forward_ex(const void* q, const void* k, const void* v_t, void* out, int batch, int heads,
+                                  int seq_len, int seq_len_kv, int head_dim, int layout, int round_mode,
+                                  void* workspace, int force_split_ways, void* stream) {
+  switch (round_mode) {
+    case 0:
+      return launch_fwd<mm::kRTNE>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, layout, workspace,
+                                   force_split_ways, stream);
+    case 1:
+      return launch_fwd<mm::kRTNA>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, layout, workspace,
+                                   force_split_ways, stream);
+    case 2:
+      return launch_fwd<mm::kRTZ>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, layout, workspace,
+                                  force_split_ways, stream);
+    default:
+      return 10;
+  }
+}
+
+int moonmath_attention_plan_tail(int batch, int heads, int seq_len, int seq_len_kv, int enable, int force_split_ways,
+                                 int* out4) {
+  if (!out4 || batch <= 0 || heads <= 0 || seq_len <= 0 || seq_len_kv <= 0) return 1;
+  const int nqb = (seq_len + kRowsPerCta - 1) / kRowsPerCta;
+  const int nkb = (seq_len_kv + kKvBlock - 1) / kKvBlock;
+  const TailPlan tp = plan_tail(nqb, batch * heads, nkb, kSlots, enable != 0, force_split_ways);
+  out4[0] = tp.prefix_wgs;
+  out4[1] = tp.tail;
+  out4[2] = tp.split_ways;
+  out4[3] = tp.parts;
+  return 0;
+}
+
+int moonmath_attention_geometry(int* out4) {
+  if (!out4) return 1;
+  out4[0] = kRowsPerCta;
+  out4[1] = kKvBlock;
+  out4[2] = kSlots;
+  out4[3] = kMaxParts;
+  return 0;
+}
+
+size_t moonmath_attention_vt_bytes(int batch, int heads, int seq_len_kv) {
+  if (batch <= 0 || heads <= 0 || seq_len_kv <= 0) return 0;
+  const size_t nkb = (size_t)(seq_len_kv + kKvBlock - 1) / kKvBlock;
+  return (size_t)batch * heads * nkb * kVtBlockElems * 2;
+}
+
+}  // extern "C"

@@ -1,0 +1,141 @@
+// Shared gfx950 (CDNA4) building blocks for the moonmath kernels: vector types,
+// MFMA wrappers, per-mode fp32 -> bf16 rounding, LDS DMA, barriers, XCD remap.
+//
+// Everything here is written for gfx950 only (wave64, 32x32x16 / 16x16x32 bf16
+// MFMA, 16-byte global->LDS DMA, v_permlane32_swap).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define MM_LDS __attribute__((address_space(3)))
+
+// Round modes, numbered as in the C ABI (0 = RTNE, 1 = RTNA, 2 = RTZ).
+enum RoundMode : int { kRTNE = 0, kRTNA = 1, kRTZ = 2 };
+
+constexpr uint32_t kBf16CanonNaN = 0x7FFFu;
+constexpr float kNegFltMax = -3.402823466e+38f;
+
+// ---------------------------------------------------------------------------
+// fp32 -> bf16 bit rules (moonmath reference csrc/attention_kernel.hip:110-145):
+//   RTNE: u + 0x7FFF + ((u >> 16) & 1), keep the top 16 bits
+//   RTNA: u + 0x8000
+//   RTZ : u (truncate)
+// The "canon" variant maps every NaN to 0x7FFF in all three modes.
+// ---------------------------------------------------------------------------
+template <int MODE>
+__device__ __forceinline__ uint32_t bf16_bits_raw(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if constexpr (MODE == kRTNE) {
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  } else if constexpr (MODE == kRTNA) {
+    return (u + 0x8000u) >> 16;
+  } else {
+    return u >> 16;
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ uint32_t bf16_bits_canon(float f) {
+  // The NaN test is done on bits so no compiler flag can fold it away.
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const bool is_nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
+  return is_nan ? kBf16CanonNaN : bf16_bits_raw<MODE>(f);
+}
+
+// Pack two fp32 into one dword of two bf16 (lo = a, hi = b).
+// RTNE uses the gfx950 hardware convert (v_cvt_pk_bf16_f32), which is IEEE
+// round-to-nearest-even and keeps NaN a NaN; RTNA/RTZ use the integer rules.
+template <int MODE>
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  if constexpr (MODE == kRTNE) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    bf16x2 v;
+    v[0] = (__bf16)a;
+    v[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, v);
+  } else if constexpr (MODE == kRTNA) {
+    const uint32_t ua = __builtin_bit_cast(uint32_t, a) + 0x8000u;
+    const uint32_t ub = __builtin_bit_cast(uint32_t, b) + 0x8000u;
+    return __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+  } else {
+    const uint32_t ua = __builtin_bit_cast(uint32_t, a);
+    const uint32_t ub = __builtin_bit_cast(uint32_t, b);
+    return __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ uint32_t pack2_bf16_canon(float a, float b) {
+  return bf16_bits_canon<MODE>(a) | (bf16_bits_canon<MODE>(b) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane: combine lane l with lane l^32 (v_permlane32_swap on gfx950).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xor32_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto pr = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)pr[0]), __builtin_bit_cast(float, (uint32_t)pr[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto pr = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  // pr[0] holds the low half in both halves, pr[1] the high half: the sum is
+  // formed in the same order (lo + hi) in every lane.
+  return __builtin_bit_cast(float, (uint32_t)pr[0]) + __builtin_bit_cast(float, (uint32_t)pr[1]);
+}
+
+// ---------------------------------------------------------------------------
+// Global -> LDS DMA, 16 bytes per lane. Lane l's 16 bytes land at
+// lds_dst + 16*l; lds_dst must be wave-uniform.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dma16(const void* gsrc, MM_LDS void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, lds_dst, 16, 0, 0);
+}
+
+// Barrier without the implicit vmcnt(0) that __syncthreads() carries, so
+// prefetch DMA stays in flight across it. VMEM_LEFT = loads allowed to remain
+// outstanding (issued after the data the barrier publishes).
+template <int VMEM_LEFT>
+__device__ __forceinline__ void wait_vmem_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(VMEM_LEFT) : "memory");
+}
+__device__ __forceinline__ void lds_reads_done_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// XCD-aware work remap. Workgroups are dispatched round-robin over the 8 XCDs
+// (blockIdx % 8). Remap so that XCD x runs a contiguous range of logical work
+// ids, keeping the q-blocks of one (b, h) head on one XCD and its K/V in that
+// XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int kNumXcds = 8;
+__device__ __forceinline__ int xcd_remap(int idx, int total) {
+  const int xcd = idx % kNumXcds;
+  const int pos = idx / kNumXcds;
+  const int per = total / kNumXcds;
+  const int rem = total % kNumXcds;
+  return (xcd < rem) ? xcd * (per + 1) + pos : rem * (per + 1) + (xcd - rem) * per + pos;
+}
+
+}  // namespace mm

@@ -1,0 +1,85 @@
+"""ctypes binding of ``libmoonmath_gfx950.so`` (the C ABI in include/moonmath_gfx950.h).
+
+Replaces the reference's pybind ``moonmath_attention._C`` extension
+(moonmath reference csrc/attention_api.cpp:441-473,
+csrc/mla_decode_a16w8_api.cpp:152-178, csrc/mla_decode_a16w8_multiq_api.cpp:177-196).
+The library is loaded once; a missing or incomplete library raises ImportError
+at import time -- there is no fallback path.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MOONMATH_LIB", os.path.join(_HERE, "libmoonmath_gfx950.so"))
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes)
+SIGNATURES = {}
+for _m in ("rtne", "rtna", "rtz"):
+    SIGNATURES[f"launch_v_transpose_{_m}"] = (_i, [_p, _p, _i, _i, _i, _i, _p])
+    SIGNATURES[f"launch_attention_forward_{_m}"] = (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p])
+    SIGNATURES[f"tail_workspace_bytes_{_m}"] = (_sz, [])
+SIGNATURES.update({
+    "moonmath_attention_forward_ex": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
+    "moonmath_attention_plan_tail": (_i, [_i, _i, _i, _i, _i, _i, _ip]),
+    "moonmath_attention_geometry": (_i, [_ip]),
+    "moonmath_attention_vt_bytes": (_sz, [_i, _i, _i]),
+})
+
+
+class _Lib:
+    def __init__(self, path):
+        if not os.path.exists(path):
+            raise ImportError(
+                f"moonmath_attention: HIP library not found at {path}. "
+                "Build it with `python amd-kernels_amd/build_lib.py` (hipcc, gfx950)."
+            )
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        missing = []
+        for name, (res, args) in SIGNATURES.items():
+            try:
+                fn = getattr(self.dll, name)
+            except AttributeError:
+                missing.append(name)
+                continue
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, fn)
+        if missing:
+            raise ImportError(f"moonmath_attention: {path} lacks symbols {missing}; rebuild it")
+
+
+lib = _Lib(LIB_PATH)
+
+
+def stream_ptr(device):
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def geometry():
+    out = (ctypes.c_int * 4)()
+    rc = lib.moonmath_attention_geometry(out)
+    if rc != 0:
+        raise RuntimeError(f"moonmath_attention_geometry returned {rc}")
+    return {"rows_per_cta": out[0], "kv_block": out[1], "slots": out[2], "max_parts": out[3]}
+
+
+def plan_tail(batch, heads, seq_len, seq_len_kv, enable=True, force_split_ways=0):
+    out = (ctypes.c_int * 4)()
+    rc = lib.moonmath_attention_plan_tail(batch, heads, seq_len, seq_len_kv, int(enable), force_split_ways, out)
+    if rc != 0:
+        raise ValueError(f"moonmath_attention_plan_tail returned {rc}")
+    return tuple(out)

@@ -1,0 +1,186 @@
+"""Benchmark: bf16 attention forward (headline) and fp8-KV MLA decode on one MI355X.
+
+Prints ONE JSON line. ``value`` is the attention forward throughput in TFLOP/s
+(4*B*H*Sq*Skv*D per call, the reference's formula benchmark/runner.py:7,174)
+at configs[1]: BSHD (B=2, S=8192, H=24, D=128), round mode RTNE, inputs resident
+in HBM; one step = one ``moonmath_attention.forward`` call (V transpose +
+forward kernel, as the reference times it, benchmark/runner.py:176-181).
+
+``roofline`` is for the dominant kernel (the attention forward kernel alone,
+timed with HIP events on the stream it is launched on). ``cpu_baseline`` times
+the reference repo's CPU oracle formula (examples/basic.py:16-17) on a bounded
+sample of heads on this host's cores. ``mla`` carries the MLA decode line
+(HBM GB/s) when the MLA kernel is built.
+"""
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "amd-kernels_amd"))
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def attention_flops(B, H, Sq, Skv, D=128):
+    return 4.0 * B * H * Sq * Skv * D
+
+
+def bench_attention(args, torch, ma, _lib):
+    B, S, H = 2, 8192, 24
+    mode = args.mode
+    g = torch.Generator().manual_seed(42)
+    q, k, v = (torch.randn(B, S, H, 128, generator=g).to(torch.bfloat16).to("cuda:0") for _ in range(3))
+    out = torch.empty_like(q)
+    for _ in range(args.warmup):
+        ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd")
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(args.steps):
+        ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd")
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = attention_flops(B, H, S, S)
+
+    # Dominant kernel alone: forward kernel over a pre-transposed V_t, events on
+    # the launch stream (torch's current stream, passed to the C ABI).
+    vt = torch.empty(_lib.lib.moonmath_attention_vt_bytes(B, H, S) // 2, dtype=torch.bfloat16, device="cuda:0")
+    sp = _lib.stream_ptr(q.device)
+    rc = getattr(_lib.lib, f"launch_v_transpose_{mode}")(_lib.ptr(v), _lib.ptr(vt), B * H * S, S, H, 1, sp)
+    assert rc == 0, rc
+    fwd = getattr(_lib.lib, f"launch_attention_forward_{mode}")
+    reps = max(args.steps, 5)
+    for _ in range(2):
+        fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S, 128, 1, None, sp)
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record(st)
+    for _ in range(reps):
+        rc = fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S, 128, 1, None, sp)
+    k1.record(st)
+    torch.cuda.synchronize()
+    assert rc == 0, rc
+    kms = k0.elapsed_time(k1) / reps
+    achieved = flops / (kms * 1e-3) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "attn_fwd_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    return {
+        "ms": ms,
+        "value": flops / (ms * 1e-3) / 1e12,
+        "wall_s": wall,
+        "kernel_ms": kms,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+        },
+    }
+
+
+def cpu_baseline(torch, budget_s):
+    """The reference's CPU oracle formula, fp32 torch on this host, one head at a
+    time of the headline shape (S=8192), until ~budget_s seconds have elapsed."""
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    from oracle.attention import torch_formula_cpu
+
+    g = torch.Generator().manual_seed(42)
+    S = 8192
+    done, t_total = 0, 0.0
+    while t_total < budget_s and done < 48:
+        q, k, v = (torch.randn(1, 1, S, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+        t0 = time.perf_counter()
+        torch_formula_cpu(q, k, v)
+        t_total += time.perf_counter() - t0
+        done += 1
+    flops = attention_flops(1, done, S, S)
+    return {
+        "value": round(flops / t_total / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{done} of 48 heads of the (2,24,8192,128) headline shape, fp32 torch "
+                  f"softmax(q@k^T/sqrt(128))@v per head, {t_total:.1f} s",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--mode", default="rtne", choices=["rtne", "rtna", "rtz"])
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-mla", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import moonmath_attention as ma
+    from moonmath_attention import _lib
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    _log("bench: attention headline (2,8192,24,128) bshd")
+    att = bench_attention(args, torch, ma, _lib)
+    _log(f"bench: attention {att['value']:.1f} TFLOP/s, kernel {att['kernel_ms']:.3f} ms")
+    mla = None
+    if not args.no_mla and hasattr(ma, "mla_decode_a16w8_paged_dev"):
+        from moonmath_attention import _mla_bench
+
+        _log("bench: mla decode")
+        mla = _mla_bench.run(torch, ma, steps=args.steps, warmup=args.warmup)
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("bench: cpu baseline")
+        cpu = cpu_baseline(torch, args.cpu_budget)
+    line = {
+        "metric": "attn fwd TFLOP/s (% bf16 MFMA peak); MLA decode HBM GB/s (% peak)",
+        "value": round(att["value"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(att["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "attention forward BSHD B=2 S=8192 H=24 D=128 (configs[1])",
+            "round_mode": args.mode,
+            "pct_bf16_peak": round(100 * att["value"] / PEAK_BF16_TFLOPS, 2),
+        },
+        "roofline": att["roofline"],
+        "cpu_baseline": cpu,
+    }
+    if mla is not None:
+        line["mla"] = mla
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,257 @@
+"""CPU pinning of the attention oracle (no GPU).
+
+Each check is chosen so a plausible oracle mistake fails it:
+* bf16 rules: hand-derived known-answer bits (ties both ways, odd/even LSB,
+  overflow to Inf, signed zeros, Inf, NaN) and, for RTNE, torch's own cast;
+  RTNA/RTZ against exact rational rounding of random values.
+* attention: against an fp64 softmax closed form (P rounding disabled), a
+  hand-computed 1x2 case, and blocking / split invariance of the integer max.
+* V_t: the 32x32x16 MFMA lane-layout emulator reproduces P @ V from the S^T
+  accumulator registers and the V_t fragments.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import bf16 as ob
+from oracle import planner, vt_layout
+
+# (fp32 bits, RTNE, RTNA, RTZ) derived by hand from the bit rules.
+KAT = [
+    (0x3F800000, 0x3F80, 0x3F80, 0x3F80),  # 1.0
+    (0x3F808000, 0x3F80, 0x3F81, 0x3F80),  # tie, even LSB: RTNE stays, RTNA away
+    (0x3F818000, 0x3F82, 0x3F82, 0x3F81),  # tie, odd LSB: both round up
+    (0x3F807FFF, 0x3F80, 0x3F80, 0x3F80),  # just below the tie
+    (0x3F808001, 0x3F81, 0x3F81, 0x3F80),  # just above the tie
+    (0xBF808000, 0xBF80, 0xBF81, 0xBF80),  # negative tie, even LSB
+    (0xBF818000, 0xBF82, 0xBF82, 0xBF81),  # negative tie, odd LSB
+    (0x7F7FFFFF, 0x7F80, 0x7F80, 0x7F7F),  # max finite fp32 -> Inf (RTNE/RTNA)
+    (0x7F7F7FFF, 0x7F7F, 0x7F7F, 0x7F7F),  # max finite bf16 stays
+    (0x7F7F8000, 0x7F80, 0x7F80, 0x7F7F),  # halfway above bf16 max -> Inf
+    (0x00000000, 0x0000, 0x0000, 0x0000),  # +0
+    (0x80000000, 0x8000, 0x8000, 0x8000),  # -0
+    (0x7F800000, 0x7F80, 0x7F80, 0x7F80),  # +Inf
+    (0xFF800000, 0xFF80, 0xFF80, 0xFF80),  # -Inf
+    (0x00008000, 0x0000, 0x0001, 0x0000),  # subnormal tie
+    (0x00018000, 0x0002, 0x0002, 0x0001),  # subnormal tie, odd LSB
+]
+
+
+@pytest.mark.parametrize("row", KAT)
+def test_bf16_known_answers(row):
+    u, rtne, rtna, rtz = row
+    x = ob.bits_to_f32(np.array([u], dtype=np.uint32))
+    assert int(ob.round_bits(x, ob.RTNE)[0]) == rtne
+    assert int(ob.round_bits(x, ob.RTNA)[0]) == rtna
+    assert int(ob.round_bits(x, ob.RTZ)[0]) == rtz
+
+
+@pytest.mark.parametrize("mode", [ob.RTNE, ob.RTNA, ob.RTZ])
+def test_nan_canonical(mode):
+    nans = ob.bits_to_f32(np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0x7FFFFFFF, 0xFFFFFFFF], dtype=np.uint32))
+    assert np.all(ob.round_bits(nans, mode, canon=True) == 0x7FFF)
+    raw = ob.round_bits(nans, mode)
+    assert np.all(np.isnan(ob.bf16_to_f32(raw)))
+
+
+def test_rtne_matches_torch_cast():
+    g = np.random.default_rng(0)
+    u = g.integers(0, 2 ** 32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    x = ob.bits_to_f32(u)
+    x = x[np.isfinite(x)]
+    ours = ob.round_bits(x, ob.RTNE)
+    theirs = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+def _exact_round(x, mode):
+    """Exact rational rounding of a finite float to bf16 (8-bit significand)."""
+    if x == 0:
+        return math.copysign(0.0, x)
+    f = Fraction(x)
+    sign = -1 if f < 0 else 1
+    a = abs(f)
+    e = math.floor(math.log2(a))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)
+    q = Fraction(2) ** (e - 7)
+    n, rem = divmod(a, q)
+    if mode == ob.RTZ:
+        r = n
+    elif mode == ob.RTNA:
+        r = n + (1 if rem >= q / 2 else 0)
+    else:
+        r = n + (1 if (rem > q / 2 or (rem == q / 2 and n % 2 == 1)) else 0)
+    return sign * float(r * q)
+
+
+@pytest.mark.parametrize("mode", [ob.RTNE, ob.RTNA, ob.RTZ])
+def test_rounding_vs_exact_rational(mode):
+    g = np.random.default_rng(mode + 1)
+    x = (g.standard_normal(3000) * np.exp2(g.integers(-20, 20, 3000))).astype(np.float32)
+    ours = ob.round_f32(x, mode).astype(np.float64)
+    exact = np.array([_exact_round(float(v), mode) for v in x])
+    assert np.array_equal(ours, exact)
+
+
+def _rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16).float().numpy()
+
+
+def test_attention_matches_fp64_softmax_without_p_rounding():
+    q, k, v = _rand((1, 2, 70, 128), 1), _rand((1, 2, 150, 128), 2), _rand((1, 2, 150, 128), 3)
+    _, pre, _ = oa.forward(q, k, v, ob.RTNE, p_round=False, aux=True)
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)) / math.sqrt(128)
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    ref = np.einsum("bhqk,bhkd->bhqd", p / p.sum(-1, keepdims=True), v.astype(np.float64))
+    assert np.max(np.abs(pre - ref)) < 1e-5 * np.max(np.abs(ref))
+
+
+def test_attention_p_rounding_effect_is_bounded():
+    """With P rounded the result moves by at most 2^-8 relative of the absolute scale."""
+    q, k, v = _rand((1, 1, 64, 128), 4), _rand((1, 1, 300, 128), 5), _rand((1, 1, 300, 128), 6)
+    _, pre, scl = oa.forward(q, k, v, ob.RTZ, aux=True)
+    _, pre_u, _ = oa.forward(q, k, v, ob.RTZ, p_round=False, aux=True)
+    assert np.all(np.abs(pre - pre_u) <= 2.0 ** -7 * scl)
+    assert np.any(pre != pre_u)  # rounding is actually applied
+
+
+def test_attention_hand_case():
+    """One query, two keys: s = (0, 128*c_inv) chosen so x = (0, 1) exactly."""
+    c = float(oa.SCALE_LOG2E)
+    q = np.zeros((1, 1, 1, 128), np.float32)
+    q[0, 0, 0, 0] = 1.0
+    k = np.zeros((1, 1, 2, 128), np.float32)
+    v = np.zeros((1, 1, 2, 128), np.float32)
+    v[0, 0, 0, 0], v[0, 0, 1, 0] = 1.0, 2.0
+    k[0, 0, 1, 0] = np.float32(1.0 / c)  # s1 * c ~= 1
+    out, pre, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
+    x1 = np.float32(np.float64(np.float32(1.0 / c)) * c)
+    m = np.ceil(x1)
+    p0, p1 = 2.0 ** (0 - m), 2.0 ** (np.float64(x1) - m)
+    assert pre[0, 0, 0, 0] == pytest.approx((p0 * 1 + p1 * 2) / (p0 + p1), rel=1e-6)
+    assert pre[0, 0, 0, 1] == 0.0
+
+
+@pytest.mark.parametrize("mode", [ob.RTNE, ob.RTNA, ob.RTZ])
+@pytest.mark.parametrize("ways", [1, 3])
+def test_blocking_and_split_invariance(mode, ways):
+    """Integer-grid max: per-block running max + pow2 rescales + split merge gives
+    the same bf16 as the final-max formula (up to fp64 summation order)."""
+    q, k, v = _rand((1, 1, 40, 128), 7, 2.0), _rand((1, 1, 700, 128), 8, 2.0), _rand((1, 1, 700, 128), 9)
+    full = oa.forward(q, k, v, mode)[0, 0]
+    blk = oa.head_forward_blocked(q[0, 0], k[0, 0], v[0, 0], mode, kv_block=64, split_ways=ways)
+    diff = np.abs(ob.bf16_to_f32(full).astype(np.float64) - ob.bf16_to_f32(blk))
+    assert (diff == 0).mean() > 0.999
+    assert np.all(diff <= ob.ulp_bf16(ob.bf16_to_f32(full)))
+
+
+def test_exact_max_policy_is_not_blocking_invariant():
+    """Counter-check: with an exact (non-integer) running max P's rounding depends
+    on the blocking, which is why the integer grid is used."""
+    q, k, v = _rand((1, 1, 40, 128), 7, 2.0), _rand((1, 1, 700, 128), 8, 2.0), _rand((1, 1, 700, 128), 9)
+    Q, K, V = q[0, 0].astype(np.float64), k[0, 0].astype(np.float64), v[0, 0].astype(np.float64)
+    c = float(oa.SCALE_LOG2E)
+    s = Q @ K.T * c
+
+    def run(block):
+        m = np.full(40, -np.inf)
+        o = np.zeros((40, 128))
+        l = np.zeros(40)
+        for r0 in range(0, 700, block):
+            sb = s[:, r0:r0 + block]
+            mn = np.maximum(m, sb.max(1))
+            o *= np.exp2(m - mn)[:, None]
+            l *= np.exp2(m - mn)
+            m = mn
+            p = np.exp2(sb - m[:, None]).astype(np.float32)
+            o += ob.round_f32(p, ob.RTZ).astype(np.float64) @ V[r0:r0 + block]
+            l += p.sum(1)
+        return o / l[:, None]
+
+    assert not np.array_equal(run(64), run(128))
+
+
+def test_nan_inf_semantics():
+    q = _rand((1, 1, 4, 128), 10)
+    k = _rand((1, 1, 6, 128), 11)
+    v = _rand((1, 1, 6, 128), 12)
+    k[0, 0, 2, 5] = np.nan
+    out = oa.forward(q, k, v, ob.RTNE)
+    assert np.all(out == 0x7FFF)  # one NaN key row poisons every query row
+    k = _rand((1, 1, 6, 128), 11)
+    k[0, 0, :, :] = -np.inf * np.sign(q[0, 0, 0])[None, :]  # all scores of row 0 -> -inf
+    k[0, 0, :, 1:] = 0
+    k[0, 0, :, 0] = -np.inf if q[0, 0, 0, 0] > 0 else np.inf
+    out, pre, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
+    row0 = ob.bf16_to_f32(out[0, 0, 0])
+    assert np.all(row0 == 0.0)  # l == 0 -> output 0 (reference :1114-1117)
+
+
+def test_vt_layout_is_a_permutation_of_each_block():
+    kv, d = vt_layout.vt_source_index()
+    flat = (kv * 128 + d).ravel()
+    assert np.array_equal(np.sort(flat), np.arange(64 * 128))
+
+
+def test_vt_layout_feeds_mfma_emulator_correctly():
+    """S^T accumulators as PV B-operands + V_t as A-operands == P @ V."""
+    rng = np.random.default_rng(3)
+    P = rng.standard_normal((32, 64))  # [q, kv] one block, one 32-row q tile
+    V = rng.standard_normal((64, 128))
+    rows, cols = vt_layout.acc_row_col()
+    acc = np.stack([P.T[32 * t:32 * t + 32][rows, cols] for t in range(2)])  # [t, lane, i]
+    vt = vt_layout.v_transpose(V)[0]
+    o = vt_layout.pv_block_emulated(acc, vt)
+    OT = np.zeros((128, 32))
+    for dt in range(4):
+        OT[32 * dt + rows, cols] = o[dt]
+    assert np.allclose(OT, (P @ V).T, atol=1e-10)
+
+
+def test_vt_zero_pads_rows_past_skv():
+    V = np.arange(77 * 128, dtype=np.float64).reshape(77, 128) + 1
+    vt = vt_layout.v_transpose(V, 77)
+    kv, d = vt_layout.vt_source_index()
+    assert np.all(vt[1][kv >= 13] == 0)
+    assert np.all(vt[1][kv < 13] != 0)
+
+
+@pytest.mark.parametrize(
+    "nqb,nbh,nkb,slots,expect",
+    [
+        (64, 48, 128, 512, (3072, 0, 1, 0)),   # 3072 CTAs tile 512 slots evenly
+        (33, 48, 8, 512, (1584, 0, 1, 0)),     # tail 48 but only 8 kv blocks
+        (40, 13, 192, 512, (520, 0, 1, 0)),    # tail 8 of 512 -> G=1 wins? no: see below
+        (40, 16, 192, 512, (512, 128, 4, 512)),
+        (500, 1, 192, 512, (500, 0, 1, 0)),    # last round 97.7% full
+    ],
+)
+def test_planner_cases(nqb, nbh, nkb, slots, expect):
+    # (40,16): 640 CTAs, tail 128; G <= 4 keeps one round: G=4 -> 48+3 = 51,
+    # G=8 -> 2 rounds x 24 + 3 = 51 (not better) -> G=4.
+    got = planner.plan_tail(nqb, nbh, nkb, slots, 1024)
+    if (nqb, nbh) == (40, 13):
+        # 520 CTAs, tail 8: G up to 64 in one round (8*64=512): span ceil(192/48)=4 at
+        # G=48 (nkb/G >= 4 caps G at 48) -> 4+3 = 7.
+        assert got == (512, 8, 48, 384)
+    else:
+        assert got == expect
+
+
+def test_planner_hand_case_reference_example():
+    """Reference comment :1359-1360 (tail=40, nkb=192, 304 CUs): G=4 beats G=1
+    (51 < 195). The full search (G <= 608/40 = 15) ends at G=15: 600 parts in
+    2 rounds x ceil(192/15) = 13 blocks + 3 = 29, below G=7 (1 x 28 + 3 = 31)
+    and G=14 (2 x 14 + 3 = 31)."""
+    got = planner.plan_tail(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608)
+    assert got == (304, 40, 15, 600)
