@@ -27,6 +27,9 @@ DEVICE_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Compiler-generated MFMAs keep their accumulators in VGPRs; AGPRs are used
+    # only by the hand-placed inline-asm accumulators.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

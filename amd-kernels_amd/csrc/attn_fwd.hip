@@ -38,18 +38,22 @@ namespace attn {
 
 constexpr int kD = 128;            // head_dim
 constexpr int kKvBlock = 64;       // kv rows per main-loop block
-constexpr int kWaves = 4;          // waves per CTA
+constexpr int kWaves = 4;          // waves per CTA (one per SIMD; two CTAs per CU)
 constexpr int kThreads = 64 * kWaves;
-constexpr int kQRowsPerTile = 32;  // q rows per 32x32 MFMA tile
+constexpr int kQRowsPerTile = 32;  // q rows per wave = one 32x32 MFMA tile
+constexpr int kRowsPerCta = kWaves * kQRowsPerTile;  // 128
 constexpr int kFragBytes = 1024;   // one 32x16 bf16 MFMA operand fragment (64 lanes x 16 B)
 constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
 constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
-constexpr int kStageBytes = kKBytes + kVBytes;
 constexpr int kVtBlockElems = kKvBlock * kD; // 8192 bf16 per V_t block
+constexpr int kLdsBytes = 2 * (kKBytes + kVBytes) + 64;  // 2-slot K and V_t rings + votes
+// Pass 0 accepts blocks whose per-lane sum of p stays <= 2^kGrowLog2, which
+// bounds every p by that value (no fp32 overflow of O for |v| < 2^90).
+constexpr float kGrowLimit = 1048576.0f;     // 2^20
 
-// Split-KV limits: partial records are laid out for CTAs of up to kMaxRows q
-// rows and kMaxParts parts.
-constexpr int kMaxRows = 256;
+// Split-KV limits: partial records are laid out for CTAs of kMaxRows q rows
+// and up to kMaxParts parts.
+constexpr int kMaxRows = kRowsPerCta;
 constexpr int kMaxParts = 1024;
 constexpr size_t kPartOFloats = (size_t)kMaxRows * kD;
 constexpr size_t kWorkspaceBytes = (size_t)kMaxParts * kMaxRows * (kD + 2) * sizeof(float);
@@ -73,158 +77,106 @@ __device__ __forceinline__ long long head_base(int b, int h, int S, int H, int b
   return bshd ? ((long long)b * S * H + h) * kD : ((long long)b * H + h) * (long long)S * kD;
 }
 
-template <int MODE, int QT>
+// One CTA = 4 waves = 128 q rows of one (b, h); two CTAs share a CU. Wave w
+// owns rows [32w, 32w+32). Per 64-row kv block j:
+//     QK(j+1) MFMAs || softmax(j) VALU      then      PV(j) MFMAs
+// K and V_t stream through 2-slot LDS rings, DMA'd one block ahead.
+//
+// Max policy: the running max m is an integer (log2 units) and is FIXED for the
+// main pass over the kv range, so O and l are never rescaled in the loop:
+// m = ceil(max of the first block) per row, and later blocks are accepted while
+// the lane's per-block sum of p stays <= kGrowLimit. If any row exceeds it the
+// waves vote through LDS and the CTA re-walks the range with an eager
+// integer-grid running max (rescales by exact powers of two). Since m is always
+// an integer, bf16(P) under any such m equals bf16(P) under the final max times
+// an exact power of two: the output does not depend on the path taken, the KV
+// blocking or the split.
+template <int MODE>
 __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb_begin, int kb_end, int part,
                                          char* lds) {
-  constexpr int kRows = kWaves * QT * kQRowsPerTile;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int r = lane & 31;  // query column owned by this lane in every tile
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31;  // query column owned by this lane
   const int g = lane >> 5;  // lane half
 
   const int b = bh / p.H, h = bh % p.H;
   const long long row_stride = p.bshd ? (long long)p.H * kD : kD;
   const uint16_t* qh = p.q + head_base(b, h, p.Sq, p.H, p.bshd);
-  const uint16_t* kh = p.k + head_base(b, h, p.Skv, p.H, p.bshd);
-  const uint16_t* vth = p.vt + (long long)bh * p.nkb * kVtBlockElems;
+  const char* kh = reinterpret_cast<const char*>(p.k + head_base(b, h, p.Skv, p.H, p.bshd));
+  const char* vth = reinterpret_cast<const char*>(p.vt + (long long)bh * p.nkb * kVtBlockElems);
   const float c = p.scale_log2e;
+  const int kv_end = p.Skv < kb_end * kKvBlock ? p.Skv : kb_end * kKvBlock;
 
-  // ---- K / V_t DMA for one kv block into one LDS stage ----------------------
-  // Stage layout: K fragments [t(2)][ds(8)] then V_t fragments [t(2)][s(2)][dt(4)],
-  // each 1 KB in lane order. Wave w moves fragments 4w..4w+3 of each.
-  auto issue_block = [&](int kb, int stage) {
-    char* st = lds + stage * kStageBytes;
+  // LDS: K ring [2] | V_t ring [2] | abort votes.
+  // K slot: row-major [64 rows][256 B], the 16-byte chunk c of row k stored at
+  // chunk position c ^ (k & 15): one DMA instruction moves 4 whole rows
+  // (coalesced 256-byte reads) and the MFMA fragment reads are conflict free.
+  // V_t slot: fragments [t(2)][s(2)][dt(4)], 1 KB each in lane order.
+  char* kring = lds;
+  char* vring = lds + 2 * kKBytes;
+  int* votes = reinterpret_cast<int*>(lds + 2 * (kKBytes + kVBytes));
+  // Lane byte offsets of this wave's 4 K-DMA instructions within a block.
+  uint32_t koff[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = wave * 4 + i;
-      const int t = f >> 3, ds = f & 7;
-      int kv = kb * kKvBlock + t * 32 + r;
-      kv = kv < p.Skv ? kv : p.Skv - 1;  // rows past Skv are masked in softmax
-      const uint16_t* src = kh + (long long)kv * row_stride + ds * 16 + g * 8;
-      dma16(src, (MM_LDS void*)(st + f * kFragBytes));
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int row = (wave * 4 + i) * 4 + (lane >> 4);
+    koff[i] = (uint32_t)(row * row_stride * 2) + (uint32_t)((((lane & 15) ^ (row & 15))) * 16);
+  }
+  const long long kblk_bytes = (long long)kKvBlock * row_stride * 2;
+  auto issue_k = [&](int kb, int slot) {
+    char* st = kring + slot * kKBytes;
+    if ((kb + 1) * kKvBlock <= p.Skv) {
+      const char* base = kh + kb * kblk_bytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = wave * 4 + i;
-      const uint16_t* src = vth + (long long)kb * kVtBlockElems + f * 512 + lane * 8;
-      dma16(src, (MM_LDS void*)(st + kKBytes + f * kFragBytes));
+      for (int i = 0; i < 4; ++i) dma16(base + koff[i], (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
+    } else {
+      // Last partial block: clamp rows past Skv (they are masked in softmax).
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = (wave * 4 + i) * 4 + (lane >> 4);
+        int kv = kb * kKvBlock + row;
+        kv = kv < p.Skv ? kv : p.Skv - 1;
+        dma16(kh + (long long)kv * row_stride * 2 + (((lane & 15) ^ (row & 15)) * 16),
+              (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
+      }
     }
+  };
+  const uint32_t voff = (uint32_t)(wave * 4 * kFragBytes + lane * 16);
+  auto issue_v = [&](int kb, int slot) {
+    char* st = vring + slot * kVBytes;
+    const char* base = vth + (long long)kb * kVBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(base + voff + i * kFragBytes, (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
   };
 
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
-  bf16x8 qf[QT][8];
-  const int q_row0 = qb * kRows + wave * QT * kQRowsPerTile;
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    int qr = q_row0 + qt * kQRowsPerTile + r;
+  bf16x8 qf[8];
+  const int q_row0 = qb * kRowsPerCta + wave * kQRowsPerTile;
+  {
+    int qr = q_row0 + r;
     qr = qr < p.Sq ? qr : p.Sq - 1;
     const uint16_t* src = qh + (long long)qr * row_stride + g * 8;
 #pragma unroll
-    for (int ds = 0; ds < 8; ++ds) qf[qt][ds] = *reinterpret_cast<const bf16x8*>(src + ds * 16);
+    for (int ds = 0; ds < 8; ++ds) qf[ds] = *reinterpret_cast<const bf16x8*>(src + ds * 16);
   }
 
-  f32x16 oacc[QT][4];
-  float row_m[QT], row_l[QT];
+  auto qk = [&](const char* kst, f32x16 (&s)[2]) {
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    row_m[qt] = kNegFltMax;
-    row_l[qt] = 0.f;
+    for (int t = 0; t < 2; ++t) s[t] = f32x16{};
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] = f32x16{};
-  }
-
-  if (kb_begin < kb_end) issue_block(kb_begin, 0);
-
-  for (int kb = kb_begin; kb < kb_end; ++kb) {
-    const int stage = (kb - kb_begin) & 1;
-    if (kb + 1 < kb_end) {
-      issue_block(kb + 1, stage ^ 1);
-      wait_vmem_barrier<8>();
-    } else {
-      wait_vmem_barrier<0>();
-    }
-    const char* kst = lds + stage * kStageBytes;
-    const char* vst = kst + kKBytes;
-
-    // ---- S^T = K Q^T ---------------------------------------------------------
-    f32x16 sacc[2][QT];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) sacc[t][qt] = f32x16{};
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + (t * 8 + ds) * kFragBytes + lane * 16);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) sacc[t][qt] = mfma32(kf, qf[qt][ds], sacc[t][qt]);
-      }
-    }
-
-    // ---- mask kv rows past Skv (last block only) ------------------------------
-    const int kv0 = kb * kKvBlock;
-    if (kv0 + kKvBlock > p.Skv) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kv = kv0 + t * 32 + (i >> 2) * 8 + g * 4 + (i & 3);
-          if (kv >= p.Skv) {
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) sacc[t][qt][i] = -__builtin_inff();
-          }
-        }
-    }
-
-    // ---- online softmax (integer-grid running max) ----------------------------
-    bf16x8 pf[QT][2][2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float bm = -__builtin_inff();
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) bm = fmaxf(bm, sacc[t][qt][i]);
-      bm = xor32_max(bm);
-      const float mb = __builtin_ceilf(bm * c);
-      const float m_old = row_m[qt];
-      const float m_new = fmaxf(m_old, mb);
-      const bool grew = m_new > m_old;
-      if (__builtin_amdgcn_ballot_w64(grew)) {
-        const float diff = m_old - m_new;  // integer-valued, <= 0 when grew
-        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
-        sc = (diff >= -126.f) ? sc : 0.f;
-        sc = grew ? sc : 1.f;
-        row_l[qt] *= sc;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[qt][dt] *= sc;
-      }
-      row_m[qt] = m_new;
-      const float neg_m = -m_new;
-      float lsum = 0.f;
+    for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e2 = 0; e2 < 4; ++e2) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][qt][8 * s + 2 * e2], c, neg_m));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][qt][8 * s + 2 * e2 + 1], c, neg_m));
-            lsum += p0;
-            lsum += p1;
-            w[e2] = pack2_bf16<MODE>(p0, p1);
-          }
-          u32x4 wv = {w[0], w[1], w[2], w[3]};
-          pf[qt][t][s] = __builtin_bit_cast(bf16x8, wv);
-        }
+        const int row = t * 32 + r;
+        const bf16x8 kf =
+            *reinterpret_cast<const bf16x8*>(kst + row * 256 + (((2 * ds + g) ^ (row & 15)) << 4));
+        s[t] = mfma32(kf, qf[ds], s[t]);
       }
-      row_l[qt] += lsum;
     }
-
-    // ---- O^T += V^T P^T ---------------------------------------------------------
+  };
+  f32x16 oacc[4];
+  auto pv = [&](const char* vst, const bf16x8 (&pp)[2][2]) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
@@ -233,70 +185,179 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         for (int s = 0; s < 2; ++s) {
           const bf16x8 vf =
               *reinterpret_cast<const bf16x8*>(vst + ((t * 2 + s) * 4 + dt) * kFragBytes + lane * 16);
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) oacc[qt][dt] = mfma32(vf, pf[qt][t][s], oacc[qt][dt]);
+          oacc[dt] = mfma32(vf, pp[t][s], oacc[dt]);
         }
       }
     }
-    lds_reads_done_barrier();
+  };
+  // Rows past kv_end get -inf scores (p = 0). Uniform branch: last block only.
+  auto mask = [&](f32x16 (&s)[2], int kb) {
+    const int kv0 = kb * kKvBlock;
+    if (kv0 + kKvBlock > kv_end) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int kv = kv0 + t * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
+          if (kv >= kv_end) s[t][e] = -__builtin_inff();
+        }
+    }
+  };
+  auto block_max = [&](const f32x16 (&s)[2]) {
+    float bm = -__builtin_inff();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bm = fmaxf(bm, s[t][e]);
+    return __builtin_ceilf(xor32_max(bm) * c);
+  };
+  float row_m = kNegFltMax, row_l = 0.f;
+  // p = 2^(s*c - m) -> bf16 P (per mode) for the PV B operand; returns the
+  // lane's fp32 sum of p over the block.
+  auto softmax = [&](const f32x16 (&s)[2], bf16x8 (&pp)[2][2]) {
+    const float neg_m = -row_m;
+    float lpart[4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        uint32_t w[4];
+        float acc = 0.f;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * ss + 2 * e2], c, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * ss + 2 * e2 + 1], c, neg_m));
+          acc += p0 + p1;
+          w[e2] = pack2_bf16<MODE>(p0, p1);
+        }
+        lpart[t * 2 + ss] = acc;
+        u32x4 wv = {w[0], w[1], w[2], w[3]};
+        pp[t][ss] = __builtin_bit_cast(bf16x8, wv);
+      }
+    }
+    return (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+  };
+
+  f32x16 sA[2], sB[2];
+  bf16x8 pf[2][2];
+  const int nblk = kb_end - kb_begin;
+  bool aborted = false;
+  if (nblk > 0) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
+    if (tid < kWaves) votes[tid] = 0;
+    issue_k(kb_begin, 0);
+    if (kb_begin + 1 < kb_end) issue_k(kb_begin + 1, 1);
+    issue_v(kb_begin, 0);
+    wait_vmem_barrier<0>();
+    qk(kring, sA);
+    mask(sA, kb_begin);
+    row_m = fmaxf(block_max(sA), kNegFltMax);
+
+    // One block: returns true when some wave voted to abort (seen one block late).
+    auto step = [&](int kb, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
+      const int i = kb - kb_begin;
+      // K(kb+1) and V(kb) have landed; every wave is done reading K(kb) and V(kb-1).
+      sched_fence();
+      lds_reads_done_barrier_vm0();
+      sched_fence();
+      const int vote_any = votes[0] | votes[1] | votes[2] | votes[3];
+      if (kb + 2 < kb_end) issue_k(kb + 2, i & 1);
+      if (kb + 1 < kb_end) issue_v(kb + 1, (i + 1) & 1);
+      mask(scur, kb);
+      qk(kring + ((i + 1) & 1) * kKBytes, snext);  // last block: stale slot, unused
+      const float lblk = softmax(scur, pf);
+      row_l += lblk;
+      votes[wave] = __builtin_amdgcn_ballot_w64(!(lblk <= kGrowLimit) && lblk == lblk) != 0;
+      pv(vring + (i & 1) * kVBytes, pf);
+      return vote_any != 0;
+    };
+    for (int kb = kb_begin; kb < kb_end && !aborted; kb += 2) {
+      aborted = step(kb, sA, sB);
+      if (!aborted && kb + 1 < kb_end) aborted = step(kb + 1, sB, sA);
+    }
+    sched_fence();
+    lds_reads_done_barrier_vm0();
+    if (!aborted) aborted = (votes[0] | votes[1] | votes[2] | votes[3]) != 0;
   }
+  if (aborted) {
+    // Fallback for rows whose max grew past kGrowLimit: walk the range again
+    // with an eager integer-grid running max; each raise rescales O and l by
+    // an exact power of two.
+    row_m = kNegFltMax;
+    row_l = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+      lds_reads_done_barrier_vm0();
+      issue_k(kb, 0);
+      issue_v(kb, 0);
+      wait_vmem_barrier<0>();
+      qk(kring, sA);
+      mask(sA, kb);
+      const float m_new = fmaxf(row_m, block_max(sA));
+      if (m_new > row_m) {
+        const float diff = row_m - m_new;  // integer-valued, < 0
+        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
+        sc = (diff >= -126.f) ? sc : 0.f;
+        row_l *= sc;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= sc;
+        row_m = m_new;
+      }
+      row_l += softmax(sA, pf);
+      pv(vring, pf);
+    }
+  }
+  sched_fence();
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
   // ---- epilogue -----------------------------------------------------------------
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) row_l[qt] = xor32_sum(row_l[qt]);
-
+  row_l = xor32_sum(row_l);
   if (part >= 0) {
     // Split part: unnormalised fp32 partials. Record layout per part:
     // O [kMaxRows][128] fp32 then (m, l) [kMaxRows][2] fp32.
     float* po = p.ws + (size_t)part * kPartOFloats;
     float* pml = p.ws + (size_t)kMaxParts * kPartOFloats + (size_t)part * kMaxRows * 2;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const int row = (wave * QT + qt) * kQRowsPerTile + r;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = dt * 32 + j * 8 + g * 4;
-          f32x4 v = {oacc[qt][dt][4 * j], oacc[qt][dt][4 * j + 1], oacc[qt][dt][4 * j + 2], oacc[qt][dt][4 * j + 3]};
-          *reinterpret_cast<f32x4*>(po + (size_t)row * kD + d) = v;
-        }
-      if (g == 0) {
-        pml[row * 2] = row_m[qt];
-        pml[row * 2 + 1] = row_l[qt];
-      }
-    }
-    return;
-  }
-
-  uint16_t* oh = p.out + head_base(b, h, p.Sq, p.H, p.bshd);
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int qr = q_row0 + qt * kQRowsPerTile + r;
-    if (qr >= p.Sq) continue;
-    const float l = row_l[qt];
-    const float inv = (l == 0.f) ? 0.f : __builtin_amdgcn_rcpf(l);
-    uint16_t* orow = oh + (long long)qr * row_stride;
+    const int row = wave * kQRowsPerTile + r;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = dt * 32 + j * 8 + g * 4;
-        u32x2 w;
-        w[0] = pack2_bf16_canon<MODE>(oacc[qt][dt][4 * j] * inv, oacc[qt][dt][4 * j + 1] * inv);
-        w[1] = pack2_bf16_canon<MODE>(oacc[qt][dt][4 * j + 2] * inv, oacc[qt][dt][4 * j + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d) = w;
+        f32x4 v = {oacc[dt][4 * j], oacc[dt][4 * j + 1], oacc[dt][4 * j + 2], oacc[dt][4 * j + 3]};
+        *reinterpret_cast<f32x4*>(po + (size_t)row * kD + d) = v;
       }
+    if (g == 0) {
+      pml[row * 2] = row_m;
+      pml[row * 2 + 1] = row_l;
+    }
+    return;
   }
+
+  const int qr = q_row0 + r;
+  if (qr >= p.Sq) return;
+  const float inv = (row_l == 0.f) ? 0.f : __builtin_amdgcn_rcpf(row_l);
+  uint16_t* orow = p.out + head_base(b, h, p.Sq, p.H, p.bshd) + (long long)qr * row_stride;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = dt * 32 + j * 8 + g * 4;
+      u32x2 w;
+      w[0] = pack2_bf16_canon<MODE>(oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv);
+      w[1] = pack2_bf16_canon<MODE>(oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
+      *reinterpret_cast<u32x2*>(orow + d) = w;
+    }
 }
 
-template <int MODE, int QT, int MINB>
-__global__ __launch_bounds__(kThreads, MINB) void attn_fwd_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStageBytes];
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   const int idx = blockIdx.x;
   if (idx < p.prefix_wgs) {
     const int w = xcd_remap(idx, p.prefix_wgs);
-    run_tile<MODE, QT>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
+    run_tile<MODE>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
   } else {
     // Split part: tail q-block t, part j of G, contiguous kv-block range.
     const int part = idx - p.prefix_wgs;
@@ -304,7 +365,7 @@ __global__ __launch_bounds__(kThreads, MINB) void attn_fwd_kernel(Params p) {
     const int w = p.prefix_wgs + t;
     const int kb0 = (int)((long long)p.nkb * j / p.split_ways);
     const int kb1 = (int)((long long)p.nkb * (j + 1) / p.split_ways);
-    run_tile<MODE, QT>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
+    run_tile<MODE>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
   }
 }
 
@@ -419,9 +480,7 @@ using namespace mm::attn;
 constexpr int kNumCUs = 256;
 // Kernel variant used by the launchers: QT q-tiles of 32 rows per wave and
 // MINB CTAs resident per CU.
-constexpr int kQT = 1;
-constexpr int kMinBlocks = 2;
-constexpr int kRowsPerCta = kWaves * kQT * kQRowsPerTile;
+constexpr int kMinBlocks = 2;  // CTAs resident per CU
 constexpr int kSlots = kNumCUs * kMinBlocks;
 
 // Tail KV-split cost model (re-derived from reference
@@ -494,7 +553,7 @@ int launch_fwd(const void* q, const void* k, const void* v_t, void* out, int bat
   p.split_ways = tp.split_ways;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int grid = tp.prefix_wgs + tp.parts;
-  hipLaunchKernelGGL((attn_fwd_kernel<MODE, kQT, kMinBlocks>), dim3(grid), dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((attn_fwd_kernel<MODE>), dim3(grid), dim3(kThreads), 0, st, p);
   if (tp.parts > 0) {
     const int per_qb = kRowsPerCta * kD / 4 / kMergeThreads;
     hipLaunchKernelGGL((attn_merge_kernel<MODE>), dim3(tp.tail * per_qb), dim3(kMergeThreads), 0, st, p,

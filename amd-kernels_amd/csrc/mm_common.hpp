@@ -84,6 +84,27 @@ __device__ __forceinline__ uint32_t pack2_bf16_canon(float a, float b) {
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+// Accumulate into an AGPR-resident accumulator. Non-volatile asm, so the
+// scheduler may still interleave it with independent work. Hazards the
+// compiler cannot see through the asm are covered by the fences below.
+__device__ __forceinline__ void mfma32_acc_agpr(bf16x8 a, bf16x8 b, f32x16& acc) {
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Scheduling fence: nothing moves across it.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+// Before VALU reads an accumulator written by mfma32_acc_agpr: the 8-pass
+// 32x32x16 result needs > 18 wait states before a VALU / accvgpr read.
+__device__ __forceinline__ void mfma_result_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+// Before mfma32_acc_agpr reads VGPR/AGPR operands just written by VALU.
+__device__ __forceinline__ void mfma_operand_fence() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 4" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -121,6 +142,9 @@ __device__ __forceinline__ void wait_vmem_barrier() {
 }
 __device__ __forceinline__ void lds_reads_done_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void lds_reads_done_barrier_vm0() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------

@@ -105,7 +105,7 @@ def cpu_baseline(torch, budget_s):
     g = torch.Generator().manual_seed(42)
     S = 8192
     done, t_total = 0, 0.0
-    while t_total < budget_s and done < 48:
+    while t_total < budget_s and done < 480:
         q, k, v = (torch.randn(1, 1, S, 128, generator=g).to(torch.bfloat16) for _ in range(3))
         t0 = time.perf_counter()
         torch_formula_cpu(q, k, v)
@@ -117,7 +117,7 @@ def cpu_baseline(torch, budget_s):
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{done} of 48 heads of the (2,24,8192,128) headline shape, fp32 torch "
+        "sample": f"{done} heads (each one (b,h) slice) of the (2,24,8192,128) headline shape, fp32 torch "
                   f"softmax(q@k^T/sqrt(128))@v per head, {t_total:.1f} s",
     }
 
@@ -131,6 +131,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
+    ap.add_argument("--only", choices=["attention", "mla", "copy"], default=None,
+                    help="run one leg only (for rocprofv3 counter passes); 'copy' runs a plain "
+                         "1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -143,9 +146,26 @@ def main():
     from moonmath_attention import _lib
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
+    if args.only == "copy":
+        n = 1 << 30
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        _log(f"bench: copied {n} bytes x3 (calibration)")
+        return
+    if args.only == "mla":
+        from moonmath_attention import _mla_bench
+
+        print(json.dumps(_mla_bench.run(torch, ma, steps=args.steps, warmup=args.warmup)), flush=True)
+        return
     _log("bench: attention headline (2,8192,24,128) bshd")
     att = bench_attention(args, torch, ma, _lib)
     _log(f"bench: attention {att['value']:.1f} TFLOP/s, kernel {att['kernel_ms']:.3f} ms")
+    if args.only == "attention":
+        print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"]}), flush=True)
+        return
     mla = None
     if not args.no_mla and hasattr(ma, "mla_decode_a16w8_paged_dev"):
         from moonmath_attention import _mla_bench

@@ -62,8 +62,12 @@ def softmax_p(s32, m):
         return np.exp2(x.astype(np.float64)).astype(np.float32)
 
 
-def head_forward(Q, K, V, mode, p_round=True, aux=False, chunk=None):
-    """One head: Q [Sq,128], K/V [Skv,128] float32 (bf16-valued)."""
+def head_forward(Q, K, V, mode, p_round=True, aux=False, chunk=None, p_mode=None):
+    """One head: Q [Sq,128], K/V [Skv,128] float32 (bf16-valued).
+
+    ``p_mode`` overrides the rounding of P (tests use it to plant a mistake).
+    """
+    p_mode = mode if p_mode is None else p_mode
     Sq, Skv = Q.shape[0], K.shape[0]
     K64 = K.astype(np.float64)
     V64 = V.astype(np.float64)
@@ -79,7 +83,7 @@ def head_forward(Q, K, V, mode, p_round=True, aux=False, chunk=None):
             s32 = (Q[r0:r1].astype(np.float64) @ K64.T).astype(np.float32)
             m = row_max_int(s32)
             p = softmax_p(s32, m)
-            P = _b.round_f32(p, mode) if p_round else p
+            P = _b.round_f32(p, p_mode) if p_round else p
             P64 = P.astype(np.float64)
             num = P64 @ V64
             den = p.astype(np.float64).sum(axis=1)
@@ -92,7 +96,7 @@ def head_forward(Q, K, V, mode, p_round=True, aux=False, chunk=None):
     return out, pre, scl
 
 
-def forward(q, k, v, mode, layout="bhsd", heads=None, p_round=True, aux=False):
+def forward(q, k, v, mode, layout="bhsd", heads=None, p_round=True, aux=False, p_mode=None):
     """Full forward. q/k/v float32 arrays of bf16 values in ``layout``.
 
     ``heads``: optional list of (b, h) to compute (others left 0 / NaN scale).
@@ -100,6 +104,8 @@ def forward(q, k, v, mode, layout="bhsd", heads=None, p_round=True, aux=False):
     """
     if isinstance(mode, str):
         mode = _b.MODES[mode]
+    if isinstance(p_mode, str):
+        p_mode = _b.MODES[p_mode]
     qh, kh, vh = _to_bhsd(q, layout), _to_bhsd(k, layout), _to_bhsd(v, layout)
     B, H, Sq, _ = qh.shape
     out = np.zeros((B, H, Sq, D), dtype=np.uint16)
@@ -107,7 +113,7 @@ def forward(q, k, v, mode, layout="bhsd", heads=None, p_round=True, aux=False):
     scl = np.full((B, H, Sq, D), np.nan) if aux else None
     todo = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
     for b, h in todo:
-        o, pr, sc = head_forward(qh[b, h], kh[b, h], vh[b, h], mode, p_round=p_round, aux=aux)
+        o, pr, sc = head_forward(qh[b, h], kh[b, h], vh[b, h], mode, p_round=p_round, aux=aux, p_mode=p_mode)
         out[b, h] = o
         if aux:
             pre[b, h] = pr

@@ -255,3 +255,21 @@ def test_planner_hand_case_reference_example():
     and G=14 (2 x 14 + 3 = 31)."""
     got = planner.plan_tail(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608)
     assert got == (304, 40, 15, 600)
+
+
+@pytest.mark.parametrize("out_mode,p_mode", [(ob.RTNE, ob.RTZ), (ob.RTNA, ob.RTZ), (ob.RTZ, ob.RTNE)])
+def test_tolerance_rule_rejects_wrong_p_rounding(out_mode, p_mode):
+    """A planted mistake in the oracle (P rounded with the wrong mode) must fail
+    (RTNE and RTNA differ only on exact ties of p, about 2^-16 of terms, so that
+    pair is indistinguishable and not used)
+    the tests' tolerance rule, while the correct oracle passes against itself
+    run with a different kv blocking."""
+    from helpers import compare_bf16
+
+    q, k, v = _rand((1, 1, 64, 128), 30), _rand((1, 1, 1024, 128), 31), _rand((1, 1, 1024, 128), 32)
+    ref, _, scl = oa.forward(q, k, v, out_mode, aux=True)
+    bad = oa.forward(q, k, v, out_mode, p_mode=p_mode)
+    with pytest.raises(AssertionError):
+        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0])
+    good = oa.head_forward_blocked(q[0, 0], k[0, 0], v[0, 0], out_mode, kv_block=64, split_ways=3)
+    compare_bf16(good, ref[0, 0], scl[0, 0])
