@@ -10,5 +10,22 @@ kernels in ``libmoonmath_gfx950.so`` called through ctypes.
 """
 
 from ._kernel import forward, forward_lite
+from .mla import (
+    mla_decode_a16w8,
+    mla_decode_a16w8_multiq,
+    mla_decode_a16w8_multiq_paged_dev,
+    mla_decode_a16w8_multiq_plan_parts_q,
+    mla_decode_a16w8_paged_dev,
+    mla_decode_a16w8_plan_parts,
+    mla_decode_a16w8_plan_parts_capped,
+    mla_decode_a16w8_plan_parts_q,
+)
 
-__all__ = ["forward", "forward_lite"]
+__all__ = [
+    "forward", "forward_lite",
+    "mla_decode_a16w8", "mla_decode_a16w8_paged_dev",
+    "mla_decode_a16w8_plan_parts", "mla_decode_a16w8_plan_parts_capped",
+    "mla_decode_a16w8_plan_parts_q",
+    "mla_decode_a16w8_multiq", "mla_decode_a16w8_multiq_paged_dev",
+    "mla_decode_a16w8_multiq_plan_parts_q",
+]

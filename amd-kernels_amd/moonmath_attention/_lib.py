@@ -29,6 +29,22 @@ SIGNATURES.update({
     "moonmath_attention_plan_tail": (_i, [_i, _i, _i, _i, _i, _i, _ip]),
     "moonmath_attention_geometry": (_i, [_ip]),
     "moonmath_attention_vt_bytes": (_sz, [_i, _i, _i]),
+    # MLA decode (reference csrc/mla_decode_a16w8_api.cpp:19-33, multiq_api.cpp:22-34)
+    "mla_decode_a16w8_workspace_bytes": (_sz, []),
+    "mla_decode_a16w8_multiq_workspace_for": (_sz, [_i, _i, _i, _i]),
+    "launch_mla_decode_a16w8": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _f, _p, _p]),
+    "launch_mla_decode_a16w8_paged_dev": (
+        _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _f, _p, _p, _sz, _i]),
+    "launch_mla_decode_a16w8_multiq": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _f, _p, _p]),
+    "launch_mla_decode_a16w8_multiq_paged_dev": (
+        _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _f, _p, _p, _sz]),
+    "mla_decode_a16w8_plan_parts": (_i, [_i, _i, _i, _i]),
+    "mla_decode_a16w8_plan_parts_q": (_i, [_i, _i, _i, _i]),
+    "mla_decode_a16w8_plan_parts_capped": (_i, [_i, _i, _i, _i]),
+    "mla_decode_a16w8_multiq_plan_parts_q": (_i, [_i, _i, _i, _i]),
+    "mla_decode_a16w8_max_ctas": (_i, []),
+    "moonmath_mla_effective_parts": (_i, [_i, _i, _i, _i, _i]),
+    "moonmath_fp8e4m3_to_bf16": (_i, [_p, _p, _i, _p]),
 })
 
 

@@ -1,0 +1,228 @@
+"""GPU parity of the gfx950 MLA decode against the CPU oracle.
+
+Mirrors reference tests/test_mla_decode.py (peaked queries x3, KV = e4m3 of
+N(0,1) at kv_scale 1/32, random slot permutation, end-aligned window poison
+test, rows reversal bit-identity, domain rejections) with OCP e4m3fn KV and the
+gfx950 domain (H up to 128, multi-query q_len 2..8).
+
+Tolerance (stated for this path): the same rule as the attention forward
+(helpers.compare_bf16: 1 bf16 ULP at max(|ref|, A/4) against the oracle that
+applies the kernel's precision model -- bf16 P (RTNE), integer-grid max, fp8
+dequant -- plus >= 98% bit-exact and >= 99.5% strictly within 1 ULP), and the
+reference's own floor: rel-L2 < 3e-3 against its plain fp32 formula.
+"""
+import numpy as np
+import pytest
+import torch
+
+import moonmath_attention as ma
+from moonmath_attention import _lib
+from oracle import fp8 as of8
+from oracle import mla as om
+from helpers import bits, compare_bf16
+from mla_inputs import (KV_SCALE, QK, SCALE_192, SCALE_576, fp8_bits, paged_pool, ragged_lens, rand_kv_rows,
+                        rand_q)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+REL_L2 = 3e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+
+
+def _d(t):
+    return None if t is None else t.to(DEV)
+
+
+def _rel_l2(out, ref):
+    return float(np.linalg.norm(out.astype(np.float64) - ref) / np.linalg.norm(ref))
+
+
+def _check(o_lat, q_lat, q_pe, kv_u8, lens, scale, kv_indices=None, kv_indptr=None, rows=None, batches=None):
+    got = bits(o_lat)
+    if got.ndim == 3:
+        got = got[:, None]
+    ql = q_lat.float().numpy()
+    qp = q_pe.float().numpy()
+    if ql.ndim == 3:
+        ql, qp = ql[:, None], qp[:, None]
+    ref, _, A = om.decode(ql, qp, kv_u8, lens, scale, KV_SCALE, kv_indices=kv_indices, kv_indptr=kv_indptr,
+                          rows=rows, batches=batches, aux=True)
+    bsel = list(range(ql.shape[0])) if batches is None else list(batches)
+    qsel = bsel if rows is None else [min(max(int(rows[b]), 0), ql.shape[0] - 1) for b in bsel]
+    stats = compare_bf16(got[qsel], ref[qsel], A[qsel])
+    if rows is None and kv_indices is None:
+        f32 = om.fp32_reference(ql[bsel], qp[bsel], kv_u8[bsel], [lens[b] for b in bsel], scale, KV_SCALE)
+        stats["rel_l2"] = _rel_l2(om._b.bf16_to_f32(got[bsel]), f32)
+        assert stats["rel_l2"] < REL_L2, stats
+    return stats
+
+
+def test_fp8_hardware_convert_matches_ocp_decode():
+    """v_cvt_scalef32_pk_bf16_fp8 (scale 1) on all 256 e4m3fn codes vs the OCP table."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).to(DEV)
+    out = torch.empty(256, dtype=torch.int16, device=DEV)
+    assert _lib.lib.moonmath_fp8e4m3_to_bf16(_lib.ptr(codes), _lib.ptr(out), 256, _lib.stream_ptr(DEV)) == 0
+    torch.cuda.synchronize()
+    got = om._b.bf16_to_f32(out.cpu().numpy().view(np.uint16)).astype(np.float64)
+    exp = of8.DECODE
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], exp[~nan])
+    assert np.array_equal(np.signbit(got[~nan]), np.signbit(exp[~nan]))
+
+
+@pytest.mark.parametrize("H", [12, 16, 128])
+def test_single_query_contiguous(H):
+    B, S = 2, 2048
+    kv = rand_kv_rows(B * S, 11).view(B, S, QK)
+    q_lat, q_pe = rand_q(B, 1, H, 11)
+    q_lat, q_pe = q_lat[:, 0].contiguous(), q_pe[:, 0].contiguous()
+    o = torch.zeros(B, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8(_d(q_lat), _d(q_pe), _d(kv), o, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    print(_check(o, q_lat, q_pe, fp8_bits(kv), [S] * B, SCALE_576))
+
+
+@pytest.mark.parametrize("q_len", [2, 4, 5, 8])
+@pytest.mark.parametrize("H", [16, 128])
+def test_multiq_contiguous(q_len, H):
+    B, S = 2, 1000
+    kv = rand_kv_rows(B * S, 23).view(B, S, QK)
+    q_lat, q_pe = rand_q(B, q_len, H, 23)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8_multiq(_d(q_lat), _d(q_pe), _d(kv), o, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(kv), [S] * B, SCALE_576)
+
+
+def test_multiq_causal_window_is_end_aligned():
+    """Reference tests/test_mla_decode.py:122-138: poisoning the last q_len-1
+    rows leaves position 0 bit-identical and moves the last position."""
+    B, S, H, q_len = 1, 2048, 16, 4
+    kv = rand_kv_rows(B * S, 31).view(B, S, QK)
+    q_lat, q_pe = rand_q(B, q_len, H, 31)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    kvd = _d(kv)
+    ma.mla_decode_a16w8_multiq(_d(q_lat), _d(q_pe), kvd, o, SCALE_576, KV_SCALE)
+    base = o.clone()
+    kvd[:, S - q_len + 1:] = _d(rand_kv_rows(q_len - 1, 99)).view(1, q_len - 1, QK)
+    ma.mla_decode_a16w8_multiq(_d(q_lat), _d(q_pe), kvd, o, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:, 0].view(torch.int16), base[:, 0].view(torch.int16)), "position 0 read past its limit"
+    assert not torch.equal(o[:, -1], base[:, -1]), "last position missed the tail tokens"
+
+
+@pytest.mark.parametrize("q_len", [1, 2, 4, 8])
+def test_paged_ragged_matches_oracle(q_len):
+    B, H = 3, 16
+    lens = [2048, 2064, 1024]
+    pool, idx, indptr = paged_pool(lens, 43)
+    q_lat, q_pe = rand_q(B, q_len, H, 43)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    parts = ma.mla_decode_a16w8_plan_parts_q(B, max(lens), q_len, H)
+    assert parts >= 1
+    if q_len == 1:
+        ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool),
+                                      o[:, 0], _d(lens_t), None, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    else:
+        ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(lens_t), None, _d(idx),
+                                             _d(indptr), parts, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+@pytest.mark.parametrize("parts", [1, 3, 7])
+def test_split_parts_agree(parts):
+    """Any parts >= 1 gives results within the tolerance rule of parts = 1."""
+    B, H, q_len = 2, 32, 2
+    lens = [1500, 700]
+    pool, idx, indptr = paged_pool(lens, 47)
+    q_lat, q_pe = rand_q(B, q_len, H, 47)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(torch.tensor(lens, dtype=torch.int32)),
+                                         None, _d(idx), _d(indptr), parts, SCALE_192, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_192, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+def test_paged_rows_remaps_query_and_output():
+    """Reference tests/test_mla_decode.py:164-188: reversing rows reverses the batch."""
+    B, H, q_len = 4, 16, 4
+    lens = [2048] * B
+    pool, idx, indptr = paged_pool(lens, 57)
+    q_lat, q_pe = rand_q(B, q_len, H, 57)
+    lens_t = _d(torch.tensor(lens, dtype=torch.int32))
+    parts = ma.mla_decode_a16w8_multiq_plan_parts_q(B, lens[0], q_len, H)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, lens_t, None, _d(idx), _d(indptr),
+                                         parts, SCALE_576, KV_SCALE)
+    rows = _d(torch.arange(B - 1, -1, -1, dtype=torch.int32))
+    o_rev = torch.zeros_like(o)
+    ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat.flip(0).contiguous()), _d(q_pe.flip(0).contiguous()), _d(pool),
+                                         o_rev, lens_t, rows, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o_rev.flip(0).view(torch.int16), o.view(torch.int16))
+
+
+@pytest.mark.parametrize("q_len", [1, 2])
+def test_deepseek_config_sampled(q_len):
+    """B=64, H=128, ctx ~ U[1024, 8192], 64-token pages over a
+    permuted pool, scale 1/sqrt(192); 4 sampled requests vs the oracle, and
+    run-to-run determinism."""
+    B, H = 64, 128
+    lens = ragged_lens(B, 1024, 8192, seed=5)
+    pool, idx, indptr = paged_pool(lens, 61)
+    q_lat, q_pe = rand_q(B, q_len, H, 61, peak=1.0)
+    lens_t = _d(torch.tensor(lens, dtype=torch.int32))
+    parts = ma.mla_decode_a16w8_plan_parts_q(B, 8192, q_len, H)
+    args = (_d(pool), None, lens_t, None, _d(idx), _d(indptr), parts, SCALE_192, KV_SCALE)
+    o1 = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    o2 = torch.zeros_like(o1)
+    fn = ma.mla_decode_a16w8_multiq_paged_dev if q_len > 1 else ma.mla_decode_a16w8_paged_dev
+    qd, pd = _d(q_lat), _d(q_pe)
+    if q_len == 1:
+        qd, pd = qd[:, 0].contiguous(), pd[:, 0].contiguous()
+    for o in (o1, o2):
+        oo = o[:, 0] if q_len == 1 else o
+        fn(qd, pd, args[0], oo, args[2], None, args[4], args[5], parts, SCALE_192, KV_SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), "not deterministic"
+    print(_check(o1, q_lat, q_pe, fp8_bits(pool), lens, SCALE_192, kv_indices=idx.numpy(),
+                 kv_indptr=indptr.numpy(), batches=[0, 17, 40, 63]))
+
+
+# ---- supported domain (reference tests/test_mla_decode.py:194-220) -------------
+
+
+@pytest.mark.parametrize("q_len", [1, 9])
+def test_multiq_rejects_q_len_out_of_domain(q_len):
+    B, S, H = 1, 256, 16
+    kv = _d(rand_kv_rows(B * S, 71).view(B, S, QK))
+    q_lat, q_pe = rand_q(B, q_len, H, 71)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="q_len"):
+        ma.mla_decode_a16w8_multiq(_d(q_lat), _d(q_pe), kv, o, SCALE_576, KV_SCALE)
+
+
+def test_multiq_rejects_too_many_heads():
+    B, S, q_len = 1, 256, 4
+    kv = _d(rand_kv_rows(B * S, 73).view(B, S, QK))
+    q_lat, q_pe = rand_q(B, q_len, 129, 73)
+    o = torch.zeros(B, q_len, 129, 512, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="H must be"):
+        ma.mla_decode_a16w8_multiq(_d(q_lat), _d(q_pe), kv, o, SCALE_576, KV_SCALE)
+
+
+def test_multiq_rejects_q_len_1_rank():
+    B, S, H = 1, 256, 16
+    kv = _d(rand_kv_rows(B * S, 79).view(B, S, QK))
+    q_lat, q_pe = rand_q(B, 1, H, 79)
+    o = torch.zeros(B, H, 512, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match=r"\[B,q_len,H,512\]"):
+        ma.mla_decode_a16w8_multiq(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), kv, o, SCALE_576,
+                                   KV_SCALE)
