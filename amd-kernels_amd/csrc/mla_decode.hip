@@ -50,6 +50,9 @@ constexpr int kKTileBytes = 2 * kKSteps * 64 * 16;           // 36864: bf16 K fr
 constexpr int kVTileBytes = kDTiles * 64 * 16;               // 32768: bf16 V^T fragments [dt][lane]
 constexpr int kDmaPieces = kStageBytes / 16;                 // 1152 16-byte pieces per tile
 constexpr int kDmaInsts = kDmaPieces / 64;                   // 18 wave-DMA instructions per tile
+constexpr int kStages = 3;                                   // fp8 staging ring (DMA 2 tiles ahead)
+constexpr int kIdxCap = 4096;                                // slot indices resident in LDS per sub-range
+constexpr int kJunkBytes = 1024;                             // sink for padding DMAs
 
 // Split partial records: one per (b, part, query row): O [512] fp32, then all
 // (m, l) pairs after the last O record. kMaxRecords caps the workspace.
@@ -75,10 +78,14 @@ template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64, 1) void mla_decode_kernel(Params p) {
   constexpr int kThreads = WAVES * 64;
   constexpr int kQRows = WAVES * kRowsPerWave;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStageBytes + kKTileBytes + kVTileBytes];
+  constexpr int kDmaPerWave = (kDmaInsts + WAVES - 1) / WAVES;  // padded to be uniform
+  __shared__ __attribute__((aligned(1024)))
+      char lds[kStages * kStageBytes + kKTileBytes + kVTileBytes + kIdxCap * 4 + kJunkBytes];
   char* stage = lds;
-  char* ktile = lds + 2 * kStageBytes;
+  char* ktile = lds + kStages * kStageBytes;
   char* vtile = ktile + kKTileBytes;
+  int* idx_lds = reinterpret_cast<int*>(vtile + kVTileBytes);
+  char* junk = reinterpret_cast<char*>(idx_lds + kIdxCap);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -123,16 +130,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mla_decode_kernel(Params p) {
 
   // ---- DMA of one fp8 tile (32 tokens x 576 B) into a staging slot ---------------
   // Piece P = inst*64 + lane covers token P / 36, bytes (P % 36) * 16 of its row.
-  // Tokens past kv_hi are clamped to the last valid one (masked in softmax).
-  auto issue_tile = [&](int tok0, int slot) {
+  // Every wave issues kDmaPerWave instructions per tile (the padding ones land in
+  // the junk area) so vmcnt waits count whole tiles. Tokens past hi are clamped
+  // to the last valid one (masked in softmax). Paged rows come from idx_lds,
+  // which holds the slots of tokens [sub_lo, sub_lo + kIdxCap).
+  auto issue_tile = [&](int tok0, int slot, int sub_lo, int hi) {
     char* st = stage + slot * kStageBytes;
-    for (int inst = wave; inst < kDmaInsts; inst += WAVES) {
-      const int piece = inst * 64 + lane;
+#pragma unroll
+    for (int k = 0; k < kDmaPerWave; ++k) {
+      const int inst = wave + k * WAVES;
+      const int piece = (inst < kDmaInsts ? inst : 0) * 64 + lane;
       const int tok = piece / 36, chunk = piece % 36;
       int j = tok0 + tok;
-      j = j < kv_hi ? j : kv_hi - 1;
-      const long long row = p.paged ? (long long)p.kv_indices[slot0 + j] : (long long)b * p.S_fixed + j;
-      dma16(p.kv + row * kQK + chunk * 16, (MM_LDS void*)(st + inst * 1024));
+      j = j < hi ? j : hi - 1;
+      const long long row = p.paged ? (long long)idx_lds[j - sub_lo] : (long long)b * p.S_fixed + j;
+      char* dst = inst < kDmaInsts ? st + inst * 1024 : junk;
+      dma16(p.kv + row * kQK + chunk * 16, (MM_LDS void*)dst);
     }
   };
 
@@ -190,77 +203,90 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mla_decode_kernel(Params p) {
   float row_m = kNegFltMax, row_l = 0.f;
   const float c = p.score_c;
 
-  const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + kTileTok - 1) / kTileTok : 0;
-  if (ntiles > 0) issue_tile(kv_lo, 0);
-  for (int it = 0; it < ntiles; ++it) {
-    const int tok0 = kv_lo + it * kTileTok;
-    // Staging slot it&1 has landed; every wave is done with the bf16 tiles of it-1.
+  for (int sub_lo = kv_lo; sub_lo < kv_hi; sub_lo += kIdxCap) {
+    const int sub_hi = (sub_lo + kIdxCap < kv_hi) ? sub_lo + kIdxCap : kv_hi;
+    const int ntiles = (sub_hi - sub_lo + kTileTok - 1) / kTileTok;
+    // Every wave is done with the previous sub-range (LDS, DMAs).
     lds_reads_done_barrier_vm0();
-    if (it + 1 < ntiles) issue_tile(tok0 + kTileTok, (it + 1) & 1);
-    convert_tile(it & 1);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (p.paged) {
+      for (int i = tid; i < sub_hi - sub_lo; i += kThreads) idx_lds[i] = p.kv_indices[slot0 + sub_lo + i];
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    issue_tile(sub_lo, 0, sub_lo, sub_hi);
+    issue_tile(sub_lo + (ntiles > 1 ? kTileTok : 0), 1, sub_lo, sub_hi);
+    for (int it = 0; it < ntiles; ++it) {
+      const int tok0 = sub_lo + it * kTileTok;
+      // Tile it has landed (tile it+1 may still be in flight); every wave is done
+      // with the bf16 tiles of it-1.
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kDmaPerWave) : "memory");
+      // Two tiles ahead into the slot of tile it-1 (past the end: harmless reload).
+      const int ahead = it + 2 < ntiles ? it + 2 : ntiles - 1;
+      issue_tile(sub_lo + ahead * kTileTok, (it + 2) % kStages, sub_lo, sub_hi);
+      convert_tile(it % kStages);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // ---- S^T = K Q^T: 2 token tiles x 18 K-steps, 4 accumulator chains --------------
-    f32x4 sacc[2][2];
+      // ---- S^T = K Q^T: 2 token tiles x 18 K-steps, 4 accumulator chains ------------
+      f32x4 sacc[2][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) sacc[tt][0] = sacc[tt][1] = f32x4{};
+      for (int tt = 0; tt < 2; ++tt) sacc[tt][0] = sacc[tt][1] = f32x4{};
 #pragma unroll
-    for (int ks = 0; ks < kKSteps; ++ks) {
+      for (int ks = 0; ks < kKSteps; ++ks) {
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ktile + ((tt * kKSteps + ks) * 64 + lane) * 16);
-        sacc[tt][ks & 1] = mfma16(kf, qf[ks], sacc[tt][ks & 1]);
+        for (int tt = 0; tt < 2; ++tt) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ktile + ((tt * kKSteps + ks) * 64 + lane) * 16);
+          sacc[tt][ks & 1] = mfma16(kf, qf[ks], sacc[tt][ks & 1]);
+        }
+      }
+      float s[8];  // e = tt*4 + i  <->  token tok0 + 16tt + 4g + i
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = tok0 + tt * 16 + 4 * g + i;
+          const float v = sacc[tt][0][i] + sacc[tt][1][i];
+          s[tt * 4 + i] = (tok < lim && tok < sub_hi) ? v : -__builtin_inff();
+        }
+
+      // ---- online softmax (integer-grid running max) --------------------------------
+      float bm = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bm = fmaxf(bm, s[e]);
+      bm = fmaxf(bm, __shfl_xor(bm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32));
+      const float m_new = fmaxf(row_m, __builtin_ceilf(bm * c));
+      const bool grow = m_new > row_m;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float diff = row_m - m_new;  // integer-valued, <= 0
+        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
+        sc = (diff >= -126.f) ? sc : 0.f;
+        sc = grow ? sc : 1.f;
+        row_l *= sc;
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] *= sc;
+        row_m = m_new;
+      }
+      const float neg_m = -row_m;
+      float pv[8];
+      float lsum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], c, neg_m));
+        lsum += pv[e];
+      }
+      row_l += lsum;
+      u32x4 pw = {pack2_bf16<kRTNE>(pv[0], pv[1]), pack2_bf16<kRTNE>(pv[2], pv[3]),
+                  pack2_bf16<kRTNE>(pv[4], pv[5]), pack2_bf16<kRTNE>(pv[6], pv[7])};
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
+
+      // ---- O^T += V^T P^T: 32 independent d-tile accumulators -------------------------
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) {
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vtile + (dt * 64 + lane) * 16);
+        oacc[dt] = mfma16(vf, pf, oacc[dt]);
       }
     }
-    float s[8];  // e = tt*4 + i  <->  token tok0 + 16tt + 4g + i
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + tt * 16 + 4 * g + i;
-        const float v = sacc[tt][0][i] + sacc[tt][1][i];
-        s[tt * 4 + i] = (tok < lim && tok < kv_hi) ? v : -__builtin_inff();
-      }
-
-    // ---- online softmax (integer-grid running max) ----------------------------------
-    float bm = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bm = fmaxf(bm, s[e]);
-    bm = fmaxf(bm, __shfl_xor(bm, 16));
-    bm = fmaxf(bm, __shfl_xor(bm, 32));
-    const float m_new = fmaxf(row_m, __builtin_ceilf(bm * c));
-    const bool grow = m_new > row_m;
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float diff = row_m - m_new;  // integer-valued, <= 0
-      float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
-      sc = (diff >= -126.f) ? sc : 0.f;
-      sc = grow ? sc : 1.f;
-      row_l *= sc;
-#pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] *= sc;
-      row_m = m_new;
-    }
-    const float neg_m = -row_m;
-    float pv[8];
-    float lsum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], c, neg_m));
-      lsum += pv[e];
-    }
-    row_l += lsum;
-    u32x4 pw = {pack2_bf16<kRTNE>(pv[0], pv[1]), pack2_bf16<kRTNE>(pv[2], pv[3]),
-                pack2_bf16<kRTNE>(pv[4], pv[5]), pack2_bf16<kRTNE>(pv[6], pv[7])};
-    const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
-
-    // ---- O^T += V^T P^T: 32 independent d-tile accumulators ---------------------------
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vtile + (dt * 64 + lane) * 16);
-      oacc[dt] = mfma16(vf, pf, oacc[dt]);
-    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   }
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
   // ---- epilogue ---------------------------------------------------------------------------
   // Row sums: lanes n, n+16, n+32, n+48 hold partial sums of the same row.

@@ -95,6 +95,71 @@ def bench_attention(args, torch, ma, _lib):
     }
 
 
+def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
+    """B=64 absorbed-MLA paged decode, ctx ~ U[1024, 8192], 64-token
+    pages over a randomly permuted pool, OCP e4m3fn KV, scale 1/sqrt(192).
+    Three independent (Q, pool, table) sets rotate so the ~640 MB working set
+    exceeds the 256 MB Infinity Cache: each timed call streams its KV from HBM."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from mla_inputs import KV_SCALE, SCALE_192, paged_pool, ragged_lens, rand_q
+
+    B = 64
+    lens = ragged_lens(B, 1024, 8192, seed=5)
+    sum_l = sum(lens)
+    n_blocks = sum(-(-l // 64) for l in lens)
+    results = []
+    sets = []
+    for r in range(3):
+        pool, idx, indptr = paged_pool(lens, 100 + r)
+        sets.append((pool.to("cuda:0"), idx.to("cuda:0"), indptr.to("cuda:0")))
+    lens_t = torch.tensor(lens, dtype=torch.int32, device="cuda:0")
+    for H, q_len in configs:
+        qs = []
+        for r in range(3):
+            q_lat, q_pe = rand_q(B, q_len, H, 200 + r, peak=1.0)
+            o = torch.empty(B, q_len, H, 512, dtype=torch.bfloat16, device="cuda:0")
+            qs.append((q_lat.to("cuda:0"), q_pe.to("cuda:0"), o))
+        parts = ma.mla_decode_a16w8_plan_parts_q(B, 8192, q_len, H)
+
+        def call(r):
+            pool, idx, indptr = sets[r % 3]
+            q_lat, q_pe, o = qs[r % 3]
+            ma.mla_decode_a16w8_multiq_paged_dev(q_lat, q_pe, pool, o, lens_t, None, idx, indptr, parts,
+                                                 SCALE_192, KV_SCALE) if q_len > 1 else \
+                ma.mla_decode_a16w8_paged_dev(q_lat[:, 0], q_pe[:, 0], pool, o[:, 0], lens_t, None, idx, indptr,
+                                              parts, SCALE_192, KV_SCALE)
+
+        for r in range(warmup):
+            call(r)
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for r in range(steps):
+            call(r)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        # Algorithmic bytes: KV once + Q in + O out + block tables and lengths.
+        nbytes = sum_l * 576 + B * q_len * H * (576 + 512) * 2 + 4 * (n_blocks + B)
+        flops = 2.0 * (576 + 512) * H * q_len * sum_l
+        gbs = nbytes / (us * 1e-6) / 1e9
+        tfs = flops / (us * 1e-6) / 1e12
+        results.append({
+            "B": B, "H": H, "q_len": q_len, "parts": parts, "us": round(us, 2),
+            "hbm_GBs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+            "mfma_TFLOPs": round(tfs, 1), "pct_bf16_peak": round(100 * tfs / PEAK_BF16_TFLOPS, 2),
+            "bytes": nbytes,
+        })
+        _log(f"bench: mla H={H} q_len={q_len}: {us:.1f} us, {gbs:.0f} GB/s, {tfs:.0f} TFLOP/s")
+    return {
+        "metric": "MLA decode HBM GB/s (% peak)",
+        "workload": "B=64 ctx~U[1024,8192] (seed 5) 64-token pages, fp8 e4m3fn KV, 3 rotating pools",
+        "sum_ctx": sum_l,
+        "configs": results,
+    }
+
+
 def cpu_baseline(torch, budget_s):
     """The reference's CPU oracle formula, fp32 torch on this host, one head at a
     time of the headline shape (S=8192), until ~budget_s seconds have elapsed."""
@@ -156,9 +221,7 @@ def main():
         _log(f"bench: copied {n} bytes x3 (calibration)")
         return
     if args.only == "mla":
-        from moonmath_attention import _mla_bench
-
-        print(json.dumps(_mla_bench.run(torch, ma, steps=args.steps, warmup=args.warmup)), flush=True)
+        print(json.dumps(bench_mla(torch, ma, args.steps, args.warmup)), flush=True)
         return
     _log("bench: attention headline (2,8192,24,128) bshd")
     att = bench_attention(args, torch, ma, _lib)
@@ -167,11 +230,9 @@ def main():
         print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"]}), flush=True)
         return
     mla = None
-    if not args.no_mla and hasattr(ma, "mla_decode_a16w8_paged_dev"):
-        from moonmath_attention import _mla_bench
-
+    if not args.no_mla:
         _log("bench: mla decode")
-        mla = _mla_bench.run(torch, ma, steps=args.steps, warmup=args.warmup)
+        mla = bench_mla(torch, ma, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         _log("bench: cpu baseline")
