@@ -260,10 +260,9 @@ def test_planner_hand_case_reference_example():
 @pytest.mark.parametrize("out_mode,p_mode", [(ob.RTNE, ob.RTZ), (ob.RTNA, ob.RTZ), (ob.RTZ, ob.RTNE)])
 def test_tolerance_rule_rejects_wrong_p_rounding(out_mode, p_mode):
     """A planted mistake in the oracle (P rounded with the wrong mode) must fail
-    (RTNE and RTNA differ only on exact ties of p, about 2^-16 of terms, so that
-    pair is indistinguishable and not used)
     the tests' tolerance rule, while the correct oracle passes against itself
-    run with a different kv blocking."""
+    run with a different kv blocking. RTNE and RTNA differ only on exact ties of
+    p (about 2^-16 of terms), so that pair is indistinguishable and not used."""
     from helpers import compare_bf16
 
     q, k, v = _rand((1, 1, 64, 128), 30), _rand((1, 1, 1024, 128), 31), _rand((1, 1, 1024, 128), 32)
@@ -273,3 +272,27 @@ def test_tolerance_rule_rejects_wrong_p_rounding(out_mode, p_mode):
         compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0])
     good = oa.head_forward_blocked(q[0, 0], k[0, 0], v[0, 0], out_mode, kv_block=64, split_ways=3)
     compare_bf16(good, ref[0, 0], scl[0, 0])
+
+
+def _plant(kind, q, k, v, mode):
+    """The oracle with one plausible mistake planted."""
+    if kind == "dropped_term":       # last kv row left out of the sum
+        return oa.forward(q, k[:, :, :-1], v[:, :, :-1], mode)
+    if kind == "scale":              # softmax scale 1/sqrt(127) instead of 1/sqrt(128)
+        return oa.forward(q * math.sqrt(128.0 / 127.0), k, v, mode)
+    if kind == "swapped_operand":    # K used where V belongs
+        return oa.forward(q, k, k, mode)
+    if kind == "shifted_v_row":      # V indexed one row off
+        return oa.forward(q, k, np.roll(v, 1, axis=2), mode)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind", ["dropped_term", "scale", "swapped_operand", "shifted_v_row"])
+def test_tolerance_rule_rejects_planted_mistakes(kind):
+    from helpers import compare_bf16
+
+    q, k, v = _rand((1, 1, 64, 128), 40), _rand((1, 1, 300, 128), 41), _rand((1, 1, 300, 128), 42)
+    ref, _, scl = oa.forward(q, k, v, ob.RTNE, aux=True)
+    bad = _plant(kind, q, k, v, ob.RTNE)
+    with pytest.raises(AssertionError):
+        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0])
