@@ -7,27 +7,36 @@
 //
 // Replaces the reference's gfx942 single-q and multi-q kernels (moonmath
 // reference csrc/mla_decode_a16w8.hip:183-754, csrc/mla_decode_a16w8_multiq.hip
-// :282-856) with one gfx950 kernel family:
+// :282-856) with one gfx950 kernel:
 //
 //  * A query row r is (draft position t, head h) = (r / H, r % H); draft
 //    position t attends tokens [0, S - (q_len - 1 - t)) (end-aligned causal
 //    window, reference mla_decode_a16w8.hip:213-217).
-//  * One CTA = kWaves waves = kWaves*16 query rows of one request b and one KV
-//    part. The KV stream is walked in 32-token tiles: the fp8 rows are gathered
-//    by slot index into an LDS staging buffer with 16-byte DMA (double
-//    buffered), then converted ONCE per CTA (v_cvt_scalef32_pk_bf16_fp8, exact)
-//    into a bf16 K tile in MFMA fragment order and a transposed bf16 V^T tile,
-//    so the conversion is shared by every head of the CTA.
-//  * v_mfma_f32_16x16x32_bf16: S^T = K Q^T (each wave owns 16 query columns),
-//    online softmax in base 2 with the integer-grid running max (rescales are
-//    exact powers of two), P rounded to bf16 RTNE, O^T = V^T P^T with the 512
-//    output dims held as 32 independent accumulators per wave.
-//  * Split-KV: parts > 1 write unnormalised fp32 (O, m, l) per query row; the
-//    merge kernel combines them with exact power-of-two weights.
+//  * One CTA = 32 query rows of one request b and one KV part (one 32-wide
+//    v_mfma_f32_32x32x16_bf16 tile of rows). Its 4 waves (one per SIMD) walk
+//    interleaved 32-token tiles of the part: wave w takes tiles w, w+4, ...
+//    Every wave gathers its own tiles HBM -> LDS with 16-byte DMA into a private
+//    2-slot ring (the next tile is in flight while the current one is
+//    processed), so the main loop has no CTA barrier.
+//  * Operands come straight from the fp8 tile: the K fragment of a 16-dim
+//    k-step pair is one ds_read_b128 (16 fp8 of one token), the V^T fragment is
+//    one ds_read_b64_tr_b8 (8 tokens of one latent dim); both are widened with
+//    v_cvt_scalef32_pk_bf16_fp8 at scale 1, which is exact.
+//  * S^T = K Q^T accumulates in VGPRs (two chains); softmax in base 2 with
+//    each row's max m on the integer grid, m = ceil(max s * c) of the row's
+//    first non-empty tile of the wave, p = exp2(s * c - m) (<= 2^64 for later
+//    tiles, so O is never rescaled in the loop); P rounded to bf16 RTNE;
+//    O^T = V^T P^T accumulates in AGPRs (16 d-tiles x 16 fp32 per lane).
+//    Every combination of partial results uses exact power-of-two weights.
+//  * The 4 waves' (O, m, l) are merged through LDS, each wave finalising 4 of
+//    the 16 d-tiles. Split-KV parts > 1 write unnormalised fp32 (O, m, l)
+//    records that mla_merge_kernel combines with power-of-two weights.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "mm_common.hpp"
 
@@ -36,23 +45,34 @@ namespace mla {
 
 constexpr int kLat = 512;
 constexpr int kRope = 64;
-constexpr int kQK = kLat + kRope;  // 576 bytes per fp8 row
-constexpr int kTileTok = 32;       // tokens per tile
-constexpr int kKSteps = kQK / 32;  // 18 K-steps of 32 dims (16 latent + 2 rope)
-constexpr int kDTiles = kLat / 16; // 32 output d-tiles of 16
-constexpr int kRowsPerWave = 16;
+constexpr int kQK = kLat + kRope;              // 576 bytes per fp8 row
+constexpr int kTileTok = 32;                   // tokens per tile
+constexpr int kTileBytes = kTileTok * kQK;     // 18432 fp8 bytes per tile
+constexpr int kDmaPerTile = kTileBytes / 1024; // 18 wave-DMA instructions (64 x 16 B)
+constexpr int kRowsPerCta = 32;                // query rows per CTA (one MFMA tile)
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kKPairs = kQK / 32;              // 18 pairs of 16-dim k-steps (16 latent + 2 rope)
+constexpr int kDTiles = kLat / 32;             // 16 output d-tiles of 32
 constexpr int kMaxQLen = 8;
 constexpr int kMaxHeads = 128;
+constexpr int kIdxCap = 2048;                  // slot indices resident in LDS per sub-range
+// A row's running max is fixed at its first non-empty tile; later tiles may
+// exceed it by up to 2^64 (p <= 2^64, no fp32 overflow of O or l). Beyond that
+// the CTA falls back to an exact-max second pass.
+constexpr float kGrowLimit = 64.f;
 
-// LDS layout (bytes)
-constexpr int kStageBytes = kTileTok * kQK;                  // 18432: fp8 rows, token-major
-constexpr int kKTileBytes = 2 * kKSteps * 64 * 16;           // 36864: bf16 K fragments [tt][ks][lane]
-constexpr int kVTileBytes = kDTiles * 64 * 16;               // 32768: bf16 V^T fragments [dt][lane]
-constexpr int kDmaPieces = kStageBytes / 16;                 // 1152 16-byte pieces per tile
-constexpr int kDmaInsts = kDmaPieces / 64;                   // 18 wave-DMA instructions per tile
-constexpr int kStages = 3;                                   // fp8 staging ring (DMA 2 tiles ahead)
-constexpr int kIdxCap = 4096;                                // slot indices resident in LDS per sub-range
-constexpr int kJunkBytes = 1024;                             // sink for padding DMAs
+// LDS map (bytes): per-wave 2-slot tile rings, the slot indices of the current
+// sub-range, the rope part of Q. The merge at the end reuses the tile rings.
+constexpr int kRingBytes = 2 * kTileBytes;                  // 36864 per wave
+constexpr int kStageBytes = kWaves * kRingBytes;            // 147456
+constexpr int kIdxOff = kStageBytes;
+constexpr int kQpeOff = kIdxOff + kIdxCap * 4;              // 155648
+constexpr int kLdsBytes = kQpeOff + kRowsPerCta * kRope * 2;  // 159744
+// Merge area: [wave][dt][i4][lane] x 16 B of O for 8 d-tiles, then (m, l).
+constexpr int kMergeOBytes = 8 * 4 * 64 * 16;              // 32768 per wave and half
+constexpr int kMergeMlOff = kWaves * kMergeOBytes;          // 131072
+static_assert(kMergeMlOff + kWaves * 64 * 8 <= kStageBytes, "merge area fits the rings");
 
 // Split partial records: one per (b, part, query row): O [512] fp32, then all
 // (m, l) pairs after the last O record. kMaxRecords caps the workspace.
@@ -74,26 +94,56 @@ struct Params {
   float kv_scale;
 };
 
-template <int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 1) void mla_decode_kernel(Params p) {
-  constexpr int kThreads = WAVES * 64;
-  constexpr int kQRows = WAVES * kRowsPerWave;
-  constexpr int kDmaPerWave = (kDmaInsts + WAVES - 1) / WAVES;  // padded to be uniform
-  __shared__ __attribute__((aligned(1024)))
-      char lds[kStages * kStageBytes + kKTileBytes + kVTileBytes + kIdxCap * 4 + kJunkBytes];
-  char* stage = lds;
-  char* ktile = lds + kStages * kStageBytes;
-  char* vtile = ktile + kKTileBytes;
-  int* idx_lds = reinterpret_cast<int*>(vtile + kVTileBytes);
-  char* junk = reinterpret_cast<char*>(idx_lds + kIdxCap);
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Two fp8 of a dword (lo or hi half) -> two bf16, exact (scale 1).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_bf16(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+__device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
+  u32x4 o = {fp8x2_bf16<false>(lo), fp8x2_bf16<true>(lo), fp8x2_bf16<false>(hi), fp8x2_bf16<true>(hi)};
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// O^T += V^T P^T into an AGPR accumulator. The s_nop covers the VALU-write ->
+// MFMA-read distance for operands converted just before (the compiler cannot
+// see through the asm); consecutive calls always target different
+// accumulators, and every VALU read of an accumulator is preceded by
+// mfma_result_fence().
+__device__ __forceinline__ void pv_mfma(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// 16-byte global -> LDS DMA issued through asm. The kernel counts these loads
+// itself (explicit s_waitcnt vmcnt); hiding them from the compiler keeps it
+// from adding a conservative vmcnt(0) before every LDS transpose read (it
+// cannot prove those reads do not alias an in-flight DMA).
+__device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
+}
+
+// Staging layout of one tile: token t's 576-byte row at t*576, its 16-byte
+// piece c stored at piece slot c ^ swz(t) (a permutation inside each aligned
+// group of 4 pieces) so the 32 lanes of a K read and the 8-token groups of a
+// V^T transpose read hit distinct LDS banks.
+__device__ __forceinline__ int swz(int t) { return (t >> 2) & 3; }
+
+template <bool PAGED>
+__global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  int* idx_lds = reinterpret_cast<int*>(lds + kIdxOff);
+  char* qpe_lds = lds + kQpeOff;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 15;  // query column of this lane
-  const int g = lane >> 4;  // lane group (0..3)
+  const int n = lane & 31;  // MFMA column: query row (S^T, O^T) / token or dim row of A
+  const int g = lane >> 5;  // lane half
+  char* wring = lds + wave * kRingBytes;
 
-  // ---- work item: (b, part, group); groups of one (b, part) are adjacent ----
+  // ---- work item: (b, part, group); groups of one (b, part) are adjacent ------
   const int total = p.B * p.parts * p.ngroups;
   const int w = xcd_remap(blockIdx.x, total);
   const int grp = w % p.ngroups;
@@ -104,216 +154,328 @@ __global__ __launch_bounds__(WAVES * 64, 1) void mla_decode_kernel(Params p) {
     qb = p.rows[b];
     qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
   }
-  const int S = p.paged ? p.seq_lens[b] : p.S_fixed;
-  const int slot0 = p.paged ? p.kv_indptr[b] : 0;
+  const int S = PAGED ? p.seq_lens[b] : p.S_fixed;
+  const int slot0 = PAGED ? p.kv_indptr[b] : 0;
   // Proportional split: each part covers ceil(S / parts) tokens rounded to tiles.
   const int part_tok = ((S + p.parts * kTileTok - 1) / (p.parts * kTileTok)) * kTileTok;
   const int kv_lo = part * part_tok;
   const int kv_hi = (kv_lo + part_tok < S) ? kv_lo + part_tok : S;
 
-  // ---- query rows of this lane --------------------------------------------------
-  const int qrow = grp * kQRows + wave * kRowsPerWave + n;  // row within (t, h)
+  // ---- query row of this lane ----------------------------------------------------
+  const int qrow = grp * kRowsPerCta + n;  // row within (t, h)
   const bool row_ok = qrow < p.qrows;
   const int qr = row_ok ? qrow : p.qrows - 1;
   const int t_pos = qr / p.H;
   const int lim = S - (p.q_len - 1 - t_pos);  // tokens >= lim are masked for this row
-  const long long qoff = (long long)qb * p.qrows + qr;   // row index into [B, q_len, H]
+  const long long qoff = (long long)qb * p.qrows + qr;  // row index into [B, q_len, H]
 
-  // Q fragments: B operand of S^T = K Q^T, lane (n, g) holds dims 32ks + 8g .. +8.
-  bf16x8 qf[kKSteps];
+  // Q fragments (B operand of S^T = K Q^T). k-step pair s covers dims
+  // 32s + 16g .. +16 of lane half g: the first 8 feed k-step 2s, the next 8 k-step
+  // 2s+1 (the same dims the K fragment of that lane half holds).
+  bf16x8 qf[2 * (kKPairs - 2)];
 #pragma unroll
-  for (int ks = 0; ks < kKSteps; ++ks) {
-    const uint16_t* src = (ks < 16) ? p.q_lat + qoff * kLat + ks * 32 + g * 8
-                                    : p.q_pe + qoff * kRope + (ks - 16) * 32 + g * 8;
-    qf[ks] = *reinterpret_cast<const bf16x8*>(src);
+  for (int s = 0; s < kKPairs - 2; ++s) {
+    const uint16_t* src = p.q_lat + qoff * kLat + s * 32 + g * 16;
+    qf[2 * s] = *reinterpret_cast<const bf16x8*>(src);
+    qf[2 * s + 1] = *reinterpret_cast<const bf16x8*>(src + 8);
+  }
+  // Rope part of Q: 32 rows x 64 bf16 in LDS (row n at n * 128 B).
+  if (tid < kRowsPerCta * 8) {
+    const int r = tid >> 3, c = tid & 7;
+    const int rr = grp * kRowsPerCta + r;
+    const long long ro = (long long)qb * p.qrows + (rr < p.qrows ? rr : p.qrows - 1);
+    *reinterpret_cast<bf16x8*>(qpe_lds + r * 128 + c * 16) =
+        *reinterpret_cast<const bf16x8*>(p.q_pe + ro * kRope + c * 8);
   }
 
-  // ---- DMA of one fp8 tile (32 tokens x 576 B) into a staging slot ---------------
-  // Piece P = inst*64 + lane covers token P / 36, bytes (P % 36) * 16 of its row.
-  // Every wave issues kDmaPerWave instructions per tile (the padding ones land in
-  // the junk area) so vmcnt waits count whole tiles. Tokens past hi are clamped
-  // to the last valid one (masked in softmax). Paged rows come from idx_lds,
-  // which holds the slots of tokens [sub_lo, sub_lo + kIdxCap).
-  auto issue_tile = [&](int tok0, int slot, int sub_lo, int hi) {
-    char* st = stage + slot * kStageBytes;
-#pragma unroll
-    for (int k = 0; k < kDmaPerWave; ++k) {
-      const int inst = wave + k * WAVES;
-      const int piece = (inst < kDmaInsts ? inst : 0) * 64 + lane;
-      const int tok = piece / 36, chunk = piece % 36;
-      int j = tok0 + tok;
-      j = j < hi ? j : hi - 1;
-      const long long row = p.paged ? (long long)idx_lds[j - sub_lo] : (long long)b * p.S_fixed + j;
-      char* dst = inst < kDmaInsts ? st + inst * 1024 : junk;
-      dma16(p.kv + row * kQK + chunk * 16, (MM_LDS void*)dst);
-    }
-  };
+  // Retire the Q loads here, visibly to the compiler (vmcnt 0, expcnt/lgkmcnt
+  // untouched): the tile DMAs are invisible to its wait-count model, so a Q
+  // wait left to the loop would become a per-tile vmcnt countdown that also
+  // waits for the prefetched tile.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
-  // ---- fp8 staging -> bf16 K fragments and bf16 V^T fragments ------------------------
-  // K unit (tt, ks, lane=(m, g)): token 16tt + m, dims 32ks + 8g .. +8.
-  // V^T unit (dt, lane=(m, g)): dim 16dt + m, tokens tok(g, e) = 16(e/4) + 4g + e%4.
-  auto convert_tile = [&](int slot) {
-    const char* st = stage + slot * kStageBytes;
-    for (int u = tid; u < 2 * kKSteps * 64; u += kThreads) {
-      const int ln = u & 63, tk = u >> 6;  // tk = tt * 18 + ks
-      const int tt = tk / kKSteps, ks = tk % kKSteps;
-      const int tok = tt * 16 + (ln & 15);
-      const u32x2 raw = *reinterpret_cast<const u32x2*>(st + tok * kQK + ks * 32 + (ln >> 4) * 8);
-      u32x4 o;
-      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[0], 1.0f, false));
-      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[0], 1.0f, true));
-      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[1], 1.0f, false));
-      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[1], 1.0f, true));
-      *reinterpret_cast<u32x4*>(ktile + u * 16) = o;
-    }
-    // V^T: item = (d-quad dq in 0..127, group gg in 0..3): 8 tokens x 4 dims.
-    for (int it = tid; it < 128 * 4; it += kThreads) {
-      const int dq = it >> 2, gg = it & 3;
-      uint32_t rw[8];
+  // ---- per-lane constant offsets inside a staged tile -------------------------------
+  // K read of pair s: token n, piece 2s+g -> n*576 + 16*((2s+g) ^ swz(n)).
+  const int koff0 = n * kQK + 16 * (g ^ swz(n));
+  const int koff1 = n * kQK + 16 * ((2 + g) ^ swz(n));
+  // V^T transpose read (16-lane group G = 2g + mh, member j): member j supplies
+  // 8 bytes of token T = 8(e/4) + 4g + e%4 (e = j/2, +16 per k-step kk), dims
+  // 32dt + 16mh + 8(j&1) .. +8; swz(T) = 2(e/4) + g for every kk.
+  const int vj = lane & 15, vmh = (lane >> 4) & 1, ve = vj >> 1;
+  const int vT = 8 * (ve >> 2) + 4 * g + (ve & 3);
+  const int vsw = 2 * (ve >> 2) + g;
+  const int voff0 = vT * kQK + 16 * (vmh ^ vsw) + 8 * (vj & 1);
+  const int voff1 = vT * kQK + 16 * ((2 + vmh) ^ vsw) + 8 * (vj & 1);
+  // DMA: instruction k of a tile moves LDS pieces 64k .. 64k+63; with 36 pieces
+  // per row, 9 instructions cover exactly 16 token rows, so the lane pattern of
+  // k and k+9 is the same 16 rows later. dma_off[k9] = tg*576 + 16*c for the
+  // piece slot this lane fills (tg = token within the 16-row group).
+  int dma_off[9];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tok = 16 * (e >> 2) + 4 * gg + (e & 3);
-        rw[e] = *reinterpret_cast<const uint32_t*>(st + tok * kQK + dq * 4);
-      }
-      // For token pair (2k, 2k+1): bytes [A.d0, B.d0, A.d1, B.d1] and [A.d2, B.d2, A.d3, B.d3].
-      uint32_t outw[4][4];  // [dim][pair] bf16x2 (token 2k in lo, 2k+1 in hi)
-#pragma unroll
-      for (int k2 = 0; k2 < 4; ++k2) {
-        const uint32_t a = rw[2 * k2], bb = rw[2 * k2 + 1];
-        const uint32_t lo = __builtin_amdgcn_perm(bb, a, 0x05010400u);  // a.b0 b.b0 a.b1 b.b1
-        const uint32_t hi = __builtin_amdgcn_perm(bb, a, 0x07030602u);  // a.b2 b.b2 a.b3 b.b3
-        outw[0][k2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
-        outw[1][k2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
-        outw[2][k2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
-        outw[3][k2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
-      }
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd) {
-        const int d = dq * 4 + dd;
-        const int dt = d >> 4, m = d & 15;
-        u32x4 o = {outw[dd][0], outw[dd][1], outw[dd][2], outw[dd][3]};
-        *reinterpret_cast<u32x4*>(vtile + (dt * 64 + gg * 16 + m) * 16) = o;
-      }
-    }
-  };
+  for (int k9 = 0; k9 < 9; ++k9) {
+    const int pc = 64 * k9 + lane;
+    const int tg = pc / 36, cs = pc % 36;
+    dma_off[k9] = tg * kQK + 16 * (cs ^ swz(tg));
+  }
 
-  f32x4 oacc[kDTiles];
+  f32x16 oacc[kDTiles];
 #pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = f32x4{};
-  float row_m = kNegFltMax, row_l = 0.f;
+  for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = f32x16{};
+  float row_m = -__builtin_inff(), row_l = 0.f;
+  bool grew = false;  // a later tile of this row exceeded row_m by more than kGrowLimit
   const float c = p.score_c;
 
+  // One pass over the part's tiles. Accumulate mode: softmax + PV with this
+  // row's max fixed at its first non-empty tile. Max-only mode: QK and the row's
+  // largest masked score only (row_m then holds the raw score max).
+  auto sweep = [&](auto max_only_tag) {
+  constexpr bool kMaxOnly = decltype(max_only_tag)::value;
   for (int sub_lo = kv_lo; sub_lo < kv_hi; sub_lo += kIdxCap) {
     const int sub_hi = (sub_lo + kIdxCap < kv_hi) ? sub_lo + kIdxCap : kv_hi;
     const int ntiles = (sub_hi - sub_lo + kTileTok - 1) / kTileTok;
-    // Every wave is done with the previous sub-range (LDS, DMAs).
-    lds_reads_done_barrier_vm0();
-    if (p.paged) {
+    if constexpr (PAGED) {
+      lds_reads_done_barrier_vm0();  // every wave is done with the previous indices
       for (int i = tid; i < sub_hi - sub_lo; i += kThreads) idx_lds[i] = p.kv_indices[slot0 + sub_lo + i];
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      if (sub_lo == kv_lo) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // qpe_lds
     }
-    issue_tile(sub_lo, 0, sub_lo, sub_hi);
-    issue_tile(sub_lo + (ntiles > 1 ? kTileTok : 0), 1, sub_lo, sub_hi);
-    for (int it = 0; it < ntiles; ++it) {
-      const int tok0 = sub_lo + it * kTileTok;
-      // Tile it has landed (tile it+1 may still be in flight); every wave is done
-      // with the bf16 tiles of it-1.
-      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kDmaPerWave) : "memory");
-      // Two tiles ahead into the slot of tile it-1 (past the end: harmless reload).
-      const int ahead = it + 2 < ntiles ? it + 2 : ntiles - 1;
-      issue_tile(sub_lo + ahead * kTileTok, (it + 2) % kStages, sub_lo, sub_hi);
-      convert_tile(it % kStages);
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int eff = lim < sub_hi ? lim : sub_hi;  // this row's token limit in the sub-range
 
-      // ---- S^T = K Q^T: 2 token tiles x 18 K-steps, 4 accumulator chains ------------
-      f32x4 sacc[2][2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) sacc[tt][0] = sacc[tt][1] = f32x4{};
-#pragma unroll
-      for (int ks = 0; ks < kKSteps; ++ks) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ktile + ((tt * kKSteps + ks) * 64 + lane) * 16);
-          sacc[tt][ks & 1] = mfma16(kf, qf[ks], sacc[tt][ks & 1]);
+    // Gather tile j (tokens sub_lo + 32j ..) into ring slot `slot`: 18 DMAs.
+    // Fast path: the 32 rows are consecutive slots (always for the contiguous
+    // layout, and for paged tiles inside one page) -> uniform base + lane offset.
+    // Otherwise every lane looks its row up, with tokens past sub_hi clamped to
+    // the last valid one (their scores are masked).
+    auto issue_tile = [&](int j, int slot) {
+      char* dst = wring + slot * kTileBytes;
+      const int tok0 = sub_lo + j * kTileTok;
+      bool fast = tok0 + kTileTok <= sub_hi;
+      long long row0 = (long long)b * p.S_fixed + tok0;
+      if constexpr (PAGED) {
+        if (fast) {
+          const int i0 = __builtin_amdgcn_readfirstlane(idx_lds[tok0 - sub_lo]);
+          const int mine = idx_lds[tok0 - sub_lo + n];
+          fast = __builtin_amdgcn_ballot_w64(mine == i0 + n) == ~0ull;
+          row0 = i0;
         }
       }
-      float s[8];  // e = tt*4 + i  <->  token tok0 + 16tt + 4g + i
+      if (fast) {
+        const uint8_t* base = p.kv + row0 * kQK;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tok = tok0 + tt * 16 + 4 * g + i;
-          const float v = sacc[tt][0][i] + sacc[tt][1][i];
-          s[tt * 4 + i] = (tok < lim && tok < sub_hi) ? v : -__builtin_inff();
+        for (int k = 0; k < kDmaPerTile; ++k)
+          dma16_opaque(base + (k / 9) * 16 * kQK + dma_off[k % 9], dst + 1024 * k);
+      } else {
+#pragma unroll 1
+        for (int k = 0; k < kDmaPerTile; ++k) {
+          const int k9 = k % 9;
+          const int pc = 64 * k9 + lane;
+          const int tg = pc / 36, cs = pc - 36 * (pc / 36);
+          int tok = tok0 + (k / 9) * 16 + tg;
+          tok = tok < sub_hi ? tok : sub_hi - 1;
+          long long row;
+          if constexpr (PAGED) {
+            row = idx_lds[tok - sub_lo];
+          } else {
+            row = (long long)b * p.S_fixed + tok;
+          }
+          dma16_opaque(p.kv + row * kQK + 16 * (cs ^ swz(tg)), dst + 1024 * k);
         }
-
-      // ---- online softmax (integer-grid running max) --------------------------------
-      float bm = -__builtin_inff();
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bm = fmaxf(bm, s[e]);
-      bm = fmaxf(bm, __shfl_xor(bm, 16));
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
-      const float m_new = fmaxf(row_m, __builtin_ceilf(bm * c));
-      const bool grow = m_new > row_m;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float diff = row_m - m_new;  // integer-valued, <= 0
-        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
-        sc = (diff >= -126.f) ? sc : 0.f;
-        sc = grow ? sc : 1.f;
-        row_l *= sc;
-#pragma unroll
-        for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] *= sc;
-        row_m = m_new;
       }
-      const float neg_m = -row_m;
-      float pv[8];
+    };
+
+    int slot = 0;
+    if (wave < ntiles) issue_tile(wave, 0);
+    for (int j = wave; j < ntiles; j += kWaves) {
+      if (j + kWaves < ntiles) {
+        issue_tile(j + kWaves, slot ^ 1);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      const char* st = wring + slot * kTileBytes;
+      const int tok0 = sub_lo + j * kTileTok;
+
+      // ---- S^T = K Q^T: 18 k-step pairs, two accumulator chains ------------------------
+      f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+      for (int s = 0; s < kKPairs; ++s) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(st + ((s & 1) ? koff1 : koff0) + 64 * (s >> 1));
+        const bf16x8 ka = fp8x8_bf16(raw[0], raw[1]);
+        const bf16x8 kb = fp8x8_bf16(raw[2], raw[3]);
+        bf16x8 qa, qb2;
+        if (s < kKPairs - 2) {
+          qa = qf[2 * s];
+          qb2 = qf[2 * s + 1];
+        } else {
+          const char* qp = qpe_lds + n * 128 + (s - (kKPairs - 2)) * 64 + g * 32;
+          qa = *reinterpret_cast<const bf16x8*>(qp);
+          qb2 = *reinterpret_cast<const bf16x8*>(qp + 16);
+        }
+        s0 = mfma32(ka, qa, s0);
+        s1 = mfma32(kb, qb2, s1);
+      }
+      // Lane (n, g), register i: token tok0 + 8(i/4) + 4g + i%4 of query row n.
+      float sv[16];
+      const int rel = eff - tok0 - 4 * g;  // register i is valid iff 8(i/4) + i%4 < rel
+      const bool full = __builtin_amdgcn_ballot_w64(rel >= 32) == ~0ull;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float v = s0[i] + s1[i];
+        sv[i] = (full || (8 * (i >> 2) + (i & 3)) < rel) ? v : -__builtin_inff();
+      }
+
+      // ---- online softmax: running max on the integer grid, fixed per row --------------
+      float bm = sv[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) bm = fmaxf(bm, sv[i]);
+      bm = xor32_max(bm);
+      if constexpr (kMaxOnly) {
+        row_m = fmaxf(row_m, bm);
+        slot ^= 1;
+        continue;
+      }
+      const float mc = __builtin_ceilf(bm * c);
+      if (row_m == -__builtin_inff()) {
+        row_m = mc;  // first non-empty tile of the row (O and l are still 0)
+      } else {
+        grew = grew || (mc > row_m + kGrowLimit);
+      }
+      const float neg_m = (row_m == -__builtin_inff()) ? 0.f : -row_m;
+      float pv[16];
       float lsum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], c, neg_m));
-        lsum += pv[e];
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, neg_m));
+        lsum += pv[i];
       }
       row_l += lsum;
-      u32x4 pw = {pack2_bf16<kRTNE>(pv[0], pv[1]), pack2_bf16<kRTNE>(pv[2], pv[3]),
-                  pack2_bf16<kRTNE>(pv[4], pv[5]), pack2_bf16<kRTNE>(pv[6], pv[7])};
-      const bf16x8 pf = __builtin_bit_cast(bf16x8, pw);
-
-      // ---- O^T += V^T P^T: 32 independent d-tile accumulators -------------------------
+      bf16x8 pf[2];
 #pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) {
-        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(vtile + (dt * 64 + lane) * 16);
-        oacc[dt] = mfma16(vf, pf, oacc[dt]);
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4 pw = {pack2_bf16<kRTNE>(pv[8 * kk + 0], pv[8 * kk + 1]), pack2_bf16<kRTNE>(pv[8 * kk + 2], pv[8 * kk + 3]),
+                    pack2_bf16<kRTNE>(pv[8 * kk + 4], pv[8 * kk + 5]), pack2_bf16<kRTNE>(pv[8 * kk + 6], pv[8 * kk + 7])};
+        pf[kk] = __builtin_bit_cast(bf16x8, pw);
+      }
+
+      // ---- O^T += V^T P^T: 16 d-tiles x 2 token k-steps ---------------------------------
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int dt = 0; dt < kDTiles; ++dt) {
+          const char* va = st + ((dt & 1) ? voff1 : voff0) + 64 * (dt >> 1) + kk * 16 * kQK;
+          const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MM_LDS i32x2*)va);
+          pv_mfma(oacc[dt], fp8x8_bf16((uint32_t)r[0], (uint32_t)r[1]), pf[kk]);
+        }
+      }
+      slot ^= 1;
+    }
+  }
+  };
+
+  sweep(std::false_type{});
+  // Fallback (never taken unless some row's scores rise more than 2^64 above
+  // its first tile): every wave redoes its tiles with the exact row max. The
+  // decision is CTA-uniform because the sweeps hold CTA barriers.
+  {
+    int* flags = reinterpret_cast<int*>(lds + kMergeMlOff);
+    lds_reads_done_barrier_vm0();
+    if (lane == 0) flags[wave] = __builtin_amdgcn_ballot_w64(grew) != 0;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const bool retry = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+    if (retry) {
+      row_m = -__builtin_inff();
+      sweep(std::true_type{});
+      row_m = __builtin_ceilf(row_m * c);
+      row_l = 0.f;
+      mfma_result_fence();
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = f32x16{};
+      sweep(std::false_type{});
+    }
+  }
+
+  // ---- merge the 4 waves' (O, m, l) through LDS ---------------------------------------
+  // Rows of lanes n and n+32 are the same query row: m agrees, l is summed at the end.
+  mfma_result_fence();
+  lds_reads_done_barrier_vm0();  // every wave is done with its ring
+  float* mlarea = reinterpret_cast<float*>(lds + kMergeMlOff);
+  mlarea[(wave * 64 + lane) * 2] = row_m;
+  mlarea[(wave * 64 + lane) * 2 + 1] = row_l;
+  // Lane weights of the 4 waves, exact powers of two.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  float mw[kWaves], lw[kWaves];
+  float M = -__builtin_inff();
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) {
+    mw[v] = mlarea[(v * 64 + lane) * 2];
+    lw[v] = mlarea[(v * 64 + lane) * 2 + 1];
+    M = fmaxf(M, mw[v]);
+  }
+  float wt[kWaves];
+  float L = 0.f;
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) {
+    const float diff = mw[v] - M;  // integer-valued or -inf, <= 0
+    wt[v] = (mw[v] == -__builtin_inff()) ? 0.f : ((diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)diff) : 0.f);
+    L = __builtin_fmaf(wt[v], lw[v], L);
+  }
+  L = xor32_sum(L);  // whole-row sum (lanes n and n+32)
+  const bool split = p.parts > 1;
+  const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
+  const size_t rec = ((size_t)b * p.parts + part) * p.qrows + qrow;
+  uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow) * kLat;
+  float* prow = p.ws + rec * kLat;
+
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1) lds_reads_done_barrier();  // the first half's readers are done
+    // Publish this wave's 8 d-tiles of half h: [wave][dt8][i4][lane] x 16 B.
+#pragma unroll
+    for (int d8 = 0; d8 < 8; ++d8) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 v = {oacc[8 * h + d8][4 * i4], oacc[8 * h + d8][4 * i4 + 1], oacc[8 * h + d8][4 * i4 + 2],
+                         oacc[8 * h + d8][4 * i4 + 3]};
+        *reinterpret_cast<f32x4*>(lds + wave * kMergeOBytes + ((d8 * 4 + i4) * 64 + lane) * 16) = v;
       }
     }
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  }
-
-  // ---- epilogue ---------------------------------------------------------------------------
-  // Row sums: lanes n, n+16, n+32, n+48 hold partial sums of the same row.
-  row_l += __shfl_xor(row_l, 16);
-  row_l += __shfl_xor(row_l, 32);
-  if (!row_ok) return;
-  if (p.parts > 1) {
-    const size_t rec = ((size_t)b * p.parts + part) * p.qrows + qrow;
-    float* po = p.ws + rec * kLat;
-    float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + rec * 2;
+    lds_reads_done_barrier();
+    // This wave finalises d-tiles 8h + 2*wave and 8h + 2*wave + 1.
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt)
-      *reinterpret_cast<f32x4*>(po + dt * 16 + 4 * g) = oacc[dt];
-    if (g == 0) {
-      pml[0] = row_m;
-      pml[1] = row_l;
+    for (int dd = 0; dd < 2; ++dd) {
+      const int d8 = 2 * wave + dd;
+      const int dt = 8 * h + d8;
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+          const f32x4 o = *reinterpret_cast<const f32x4*>(lds + v * kMergeOBytes + ((d8 * 4 + i4) * 64 + lane) * 16);
+          acc[0] = __builtin_fmaf(wt[v], o[0], acc[0]);
+          acc[1] = __builtin_fmaf(wt[v], o[1], acc[1]);
+          acc[2] = __builtin_fmaf(wt[v], o[2], acc[2]);
+          acc[3] = __builtin_fmaf(wt[v], o[3], acc[3]);
+        }
+        // Lane (n, g), register 4*i4 + e of d-tile dt: dim 32dt + 8*i4 + 4g + e.
+        const int d = 32 * dt + 8 * i4 + 4 * g;
+        if (row_ok) {
+          if (split) {
+            *reinterpret_cast<f32x4*>(prow + d) = acc;
+          } else {
+            u32x2 o;
+            o[0] = pack2_bf16_canon<kRTNE>(acc[0] * inv, acc[1] * inv);
+            o[1] = pack2_bf16_canon<kRTNE>(acc[2] * inv, acc[3] * inv);
+            *reinterpret_cast<u32x2*>(orow + d) = o;
+          }
+        }
+      }
     }
-    return;
   }
-  const float inv = (row_l == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(row_l);
-  uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow) * kLat;
-#pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt) {
-    u32x2 o;
-    o[0] = pack2_bf16_canon<kRTNE>(oacc[dt][0] * inv, oacc[dt][1] * inv);
-    o[1] = pack2_bf16_canon<kRTNE>(oacc[dt][2] * inv, oacc[dt][3] * inv);
-    *reinterpret_cast<u32x2*>(orow + dt * 16 + 4 * g) = o;
+  if (split && row_ok && g == 0 && wave == 0) {
+    float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + rec * 2;
+    pml[0] = M;
+    pml[1] = L;
   }
 }
 
@@ -333,7 +495,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
     qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
   }
   const float* ml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat;
-  float M = kNegFltMax;
+  float M = -__builtin_inff();
   for (int j = 0; j < p.parts; ++j) {
     const size_t rec = ((size_t)b * p.parts + j) * p.qrows + qrow;
     M = fmaxf(M, ml[rec * 2]);
@@ -344,11 +506,8 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
     const size_t rec = ((size_t)b * p.parts + j) * p.qrows + qrow;
     const float m_p = ml[rec * 2];
     const float l_p = ml[rec * 2 + 1];
-    float wt = 1.f;
-    if (m_p != M) {
-      const float diff = m_p - M;
-      wt = (diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f)) : 0.f;
-    }
+    const float diff = m_p - M;  // integer-valued or -inf, <= 0
+    const float wt = (m_p == -__builtin_inff()) ? 0.f : ((diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)diff) : 0.f);
     const f32x4 o = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
     acc[0] = __builtin_fmaf(wt, o[0], acc[0]);
     acc[1] = __builtin_fmaf(wt, o[1], acc[1]);
@@ -369,8 +528,8 @@ __global__ void fp8_to_bf16_kernel(const uint8_t* in, uint16_t* out, int n) {
   if (i >= n) return;
   uint32_t v = 0;
   for (int k = 0; k < 4; ++k) v |= (uint32_t)(i + k < n ? in[i + k] : 0) << (8 * k);
-  const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, false));
-  const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, true));
+  const uint32_t lo = fp8x2_bf16<false>(v);
+  const uint32_t hi = fp8x2_bf16<true>(v);
   const uint16_t r[4] = {(uint16_t)(lo & 0xFFFF), (uint16_t)(lo >> 16), (uint16_t)(hi & 0xFFFF), (uint16_t)(hi >> 16)};
   for (int k = 0; k < 4; ++k)
     if (i + k < n) out[i + k] = r[k];
@@ -385,8 +544,7 @@ __global__ void fp8_to_bf16_kernel(const uint8_t* in, uint16_t* out, int n) {
 namespace {
 using namespace mm::mla;
 
-constexpr int kWavesPerCta = 4;
-constexpr int kQRowsPerCta = kWavesPerCta * kRowsPerWave;  // 64
+constexpr int kQRowsPerCta = kRowsPerCta;  // 32
 constexpr int kNumCUs = 256;
 constexpr int kCtasPerCu = 1;
 constexpr int kMaxParts = 64;
@@ -402,14 +560,14 @@ int max_parts_for(int B, int H, int q_len) {
 }
 
 // Split planner: enough CTAs for ~2 rounds over the CUs (ragged lengths balance
-// across rounds), at least 4 tiles per part, within the record workspace.
+// across rounds), at least 4 tiles per wave in a part, within the record workspace.
 int plan_parts(int B, int H, int max_seq_len, int q_len) {
   if (B < 1) B = 1;
   if (q_len < 1) q_len = 1;
   const int tiles = (max_seq_len + kTileTok - 1) / kTileTok;
   const int ctas_per_part = B * ngroups_for(H, q_len);
   int p = (2 * kNumCUs * kCtasPerCu + ctas_per_part - 1) / ctas_per_part;
-  if (p > tiles / 4) p = tiles / 4;
+  if (p > tiles / 16) p = tiles / 16;
   const int cap = max_parts_for(B, H, q_len);
   if (p > cap) p = cap;
   return p < 1 ? 1 : p;
@@ -456,7 +614,10 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   const long long grid = (long long)B * p.parts * p.ngroups;
   if (grid > 0x7FFFFFFFLL) return -8;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(mla_decode_kernel<kWavesPerCta>, dim3((unsigned)grid), dim3(kWavesPerCta * 64), 0, st, p);
+  if (paged)
+    hipLaunchKernelGGL(mla_decode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(mla_decode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
   if (p.parts > 1) {
     const long long cells = (long long)B * p.qrows * (kLat / 4);
     hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, st, p);
