@@ -124,6 +124,59 @@ __device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_d
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
 }
 
+// Request holding length rank `rank` (0 = longest) among B requests, in an
+// approximate longest-first order: 16 linear length buckets, longest bucket
+// first, request index order inside a bucket. Wave-uniform; every wave of a
+// CTA computes it independently from the same seq_lens.
+__device__ __forceinline__ int request_of_rank(const int* seq_lens, int B, int rank, int lane) {
+  int maxl = 0;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const int l = (c0 + lane < B) ? seq_lens[c0 + lane] : 0;
+    int m = l;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off));
+    maxl = max(maxl, m);
+  }
+  maxl = __builtin_amdgcn_readfirstlane(maxl);
+  auto bucket_of = [&](int l) {  // 0 = longest lengths
+    const long long q = (long long)l * 16 / ((long long)maxl + 1);
+    return 15 - (int)q;
+  };
+  // Bucket sizes over all requests.
+  int start[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) start[k] = 0;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const bool valid = c0 + lane < B;
+    const int bk = valid ? bucket_of(seq_lens[c0 + lane]) : -1;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) start[k] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bk == k));
+  }
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = start[k];
+    start[k] = acc;
+    acc += c;
+  }
+  // Position of every request; the one at `rank` wins.
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const bool valid = c0 + lane < B;
+    const int bk = valid ? bucket_of(seq_lens[c0 + lane]) : -1;
+    int pos = -1;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const unsigned long long m = __builtin_amdgcn_ballot_w64(bk == k);
+      if (bk == k) pos = start[k] + __builtin_popcountll(m & lt);
+      start[k] += __builtin_popcountll(m);
+    }
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(valid && pos == rank);
+    if (hit) return c0 + (int)__builtin_ctzll(hit);
+  }
+  return 0;  // unreachable for rank < B
+}
+
 // Staging layout of one tile: token t's 576-byte row at t*576, its 16-byte
 // piece c stored at piece slot c ^ swz(t) (a permutation inside each aligned
 // group of 4 pieces) so the 32 lanes of a K read and the 8-token groups of a
@@ -143,12 +196,22 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   const int g = lane >> 5;  // lane half
   char* wring = lds + wave * kRingBytes;
 
-  // ---- work item: (b, part, group); groups of one (b, part) are adjacent ------
-  const int total = p.B * p.parts * p.ngroups;
-  const int w = xcd_remap(blockIdx.x, total);
-  const int grp = w % p.ngroups;
-  const int part = (w / p.ngroups) % p.parts;
-  const int b = w / (p.ngroups * p.parts);
+  // ---- work item ----------------------------------------------------------------------
+  // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8) and in
+  // blockIdx order within an XCD. Request slots are dealt to XCDs in snake order
+  // of decreasing length (XCD x takes length ranks x, 15-x, 16+x, 31-x, ...), so
+  // every XCD gets a similar share, the E = parts * ngroups CTAs of a request
+  // run on one XCD (its KV is shared through that L2) and each XCD starts its
+  // longest requests first.
+  const int E = p.parts * p.ngroups;
+  const int xcd = blockIdx.x % kNumXcds;
+  const int k_in_xcd = blockIdx.x / kNumXcds;
+  const int tslot = k_in_xcd / E, e = k_in_xcd % E;
+  const int rank = 16 * (tslot >> 1) + ((tslot & 1) ? 15 - xcd : xcd);
+  if (rank >= p.B) return;  // padding CTA (whole CTA, before any barrier)
+  const int part = e / p.ngroups;
+  const int grp = e % p.ngroups;
+  const int b = PAGED ? request_of_rank(p.seq_lens, p.B, rank, lane) : rank;
   int qb = b;
   if (p.rows) {
     qb = p.rows[b];
@@ -242,13 +305,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     }
     const int eff = lim < sub_hi ? lim : sub_hi;  // this row's token limit in the sub-range
 
-    // Gather tile j (tokens sub_lo + 32j ..) into ring slot `slot`: 18 DMAs.
-    // Fast path: the 32 rows are consecutive slots (always for the contiguous
-    // layout, and for paged tiles inside one page) -> uniform base + lane offset.
-    // Otherwise every lane looks its row up, with tokens past sub_hi clamped to
-    // the last valid one (their scores are masked).
-    auto issue_tile = [&](int j, int slot) {
-      char* dst = wring + slot * kTileBytes;
+    // Gather plan of tile j (tokens sub_lo + 32j ..). Fast path: the 32 rows are
+    // consecutive slots (always for the contiguous layout, and for paged tiles
+    // inside one page): DMA k reads base + (k/9)*16 rows + dma_off[k%9]. Slow
+    // path: every lane looks its row up, with tokens past sub_hi clamped to the
+    // last valid one (their scores are masked).
+    auto tile_fast = [&](int j, const uint8_t*& base) -> bool {
       const int tok0 = sub_lo + j * kTileTok;
       bool fast = tok0 + kTileTok <= sub_hi;
       long long row0 = (long long)b * p.S_fixed + tok0;
@@ -260,78 +322,114 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
           row0 = i0;
         }
       }
-      if (fast) {
-        const uint8_t* base = p.kv + row0 * kQK;
-#pragma unroll
-        for (int k = 0; k < kDmaPerTile; ++k)
-          dma16_opaque(base + (k / 9) * 16 * kQK + dma_off[k % 9], dst + 1024 * k);
-      } else {
+      base = p.kv + row0 * kQK;
+      return fast;
+    };
+    auto issue_slow = [&](int j, const char* dst) {
+      const int tok0 = sub_lo + j * kTileTok;
 #pragma unroll 1
-        for (int k = 0; k < kDmaPerTile; ++k) {
-          const int k9 = k % 9;
-          const int pc = 64 * k9 + lane;
-          const int tg = pc / 36, cs = pc - 36 * (pc / 36);
-          int tok = tok0 + (k / 9) * 16 + tg;
-          tok = tok < sub_hi ? tok : sub_hi - 1;
-          long long row;
-          if constexpr (PAGED) {
-            row = idx_lds[tok - sub_lo];
-          } else {
-            row = (long long)b * p.S_fixed + tok;
-          }
-          dma16_opaque(p.kv + row * kQK + 16 * (cs ^ swz(tg)), dst + 1024 * k);
+      for (int k = 0; k < kDmaPerTile; ++k) {
+        const int k9 = k % 9;
+        const int pc = 64 * k9 + lane;
+        const int tg = pc / 36, cs = pc - 36 * (pc / 36);
+        int tok = tok0 + (k / 9) * 16 + tg;
+        tok = tok < sub_hi ? tok : sub_hi - 1;
+        long long row;
+        if constexpr (PAGED) {
+          row = idx_lds[tok - sub_lo];
+        } else {
+          row = (long long)b * p.S_fixed + tok;
         }
+        dma16_opaque(p.kv + row * kQK + 16 * (cs ^ swz(tg)), dst + 1024 * k);
+      }
+    };
+    auto issue_tile = [&](int j, const char* dst) {
+      const uint8_t* base;
+      if (tile_fast(j, base)) {
+#pragma unroll
+        for (int k = 0; k < kDmaPerTile; ++k) dma16_opaque(base + (k / 9) * 16 * kQK + dma_off[k % 9], dst + 1024 * k);
+      } else {
+        issue_slow(j, dst);
       }
     };
 
     int slot = 0;
-    if (wave < ntiles) issue_tile(wave, 0);
+    if (wave < ntiles) issue_tile(wave, wring);
     for (int j = wave; j < ntiles; j += kWaves) {
-      if (j + kWaves < ntiles) {
-        issue_tile(j + kWaves, slot ^ 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile has landed
       const char* st = wring + slot * kTileBytes;
+      const char* nst = wring + (slot ^ 1) * kTileBytes;
       const int tok0 = sub_lo + j * kTileTok;
+      // Next tile of this wave: a fast-path gather is spread over the 18 QK
+      // steps below (one DMA each); a slow-path gather is issued here.
+      const uint8_t* nbase = nullptr;
+      bool ndma = false;
+      if (j + kWaves < ntiles) {
+        ndma = tile_fast(j + kWaves, nbase);
+        if (!ndma) issue_slow(j + kWaves, nst);
+      }
 
       // ---- S^T = K Q^T: 18 k-step pairs, two accumulator chains ------------------------
+      // K pieces are read kKAhead pairs ahead of their conversion; sched_fence()
+      // keeps each step's [DMA, read ahead, convert, 2 MFMA] order.
+      constexpr int kKAhead = 4;
+      auto kaddr = [&](int s) { return st + ((s & 1) ? koff1 : koff0) + 64 * (s >> 1); };
+      u32x4 kraw[kKAhead];
+#pragma unroll
+      for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(s));
+      bf16x8 qpe[4];
       f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
       for (int s = 0; s < kKPairs; ++s) {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(st + ((s & 1) ? koff1 : koff0) + 64 * (s >> 1));
+        if (ndma) dma16_opaque(nbase + (s / 9) * 16 * kQK + dma_off[s % 9], nst + 1024 * s);
+        const u32x4 raw = kraw[s % kKAhead];
+        if (s + kKAhead < kKPairs) kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(s + kKAhead));
+        if (s == kKPairs - 2 - kKAhead) {  // rope part of Q for the last two pairs
+          const char* qp = qpe_lds + n * 128 + g * 32;
+          qpe[0] = *reinterpret_cast<const bf16x8*>(qp);
+          qpe[1] = *reinterpret_cast<const bf16x8*>(qp + 16);
+          qpe[2] = *reinterpret_cast<const bf16x8*>(qp + 64);
+          qpe[3] = *reinterpret_cast<const bf16x8*>(qp + 80);
+        }
         const bf16x8 ka = fp8x8_bf16(raw[0], raw[1]);
         const bf16x8 kb = fp8x8_bf16(raw[2], raw[3]);
-        bf16x8 qa, qb2;
-        if (s < kKPairs - 2) {
-          qa = qf[2 * s];
-          qb2 = qf[2 * s + 1];
-        } else {
-          const char* qp = qpe_lds + n * 128 + (s - (kKPairs - 2)) * 64 + g * 32;
-          qa = *reinterpret_cast<const bf16x8*>(qp);
-          qb2 = *reinterpret_cast<const bf16x8*>(qp + 16);
-        }
+        const bf16x8 qa = (s < kKPairs - 2) ? qf[2 * s] : qpe[2 * (s - (kKPairs - 2))];
+        const bf16x8 qb2 = (s < kKPairs - 2) ? qf[2 * s + 1] : qpe[2 * (s - (kKPairs - 2)) + 1];
         s0 = mfma32(ka, qa, s0);
         s1 = mfma32(kb, qb2, s1);
+        sched_fence();
       }
+      // V^T transpose reads for the first PV steps go out before the softmax.
+      constexpr int kVAhead = 8;
+      auto vaddr = [&](int i) {
+        const int kk = i / kDTiles, dt = i % kDTiles;
+        return st + ((dt & 1) ? voff1 : voff0) + 64 * (dt >> 1) + kk * 16 * kQK;
+      };
+      i32x2 vraw[kVAhead];
+#pragma unroll
+      for (int i = 0; i < kVAhead; ++i) vraw[i] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MM_LDS i32x2*)vaddr(i));
+
       // Lane (n, g), register i: token tok0 + 8(i/4) + 4g + i%4 of query row n.
       float sv[16];
-      const int rel = eff - tok0 - 4 * g;  // register i is valid iff 8(i/4) + i%4 < rel
-      const bool full = __builtin_amdgcn_ballot_w64(rel >= 32) == ~0ull;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float v = s0[i] + s1[i];
-        sv[i] = (full || (8 * (i >> 2) + (i & 3)) < rel) ? v : -__builtin_inff();
+      for (int i = 0; i < 16; ++i) sv[i] = s0[i] + s1[i];
+      const int rel = eff - tok0 - 4 * g;  // register i is valid iff 8(i/4) + i%4 < rel
+      if (__builtin_amdgcn_ballot_w64(rel < 32)) {  // the window or the range ends in this tile
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = ((8 * (i >> 2) + (i & 3)) < rel) ? sv[i] : -__builtin_inff();
       }
 
       // ---- online softmax: running max on the integer grid, fixed per row --------------
-      float bm = sv[0];
+      float mx[8];
 #pragma unroll
-      for (int i = 1; i < 16; ++i) bm = fmaxf(bm, sv[i]);
+      for (int i = 0; i < 8; ++i) mx[i] = fmaxf(sv[i], sv[i + 8]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], mx[i + 4]);
+      float bm = fmaxf(fmaxf(mx[0], mx[2]), fmaxf(mx[1], mx[3]));
       bm = xor32_max(bm);
       if constexpr (kMaxOnly) {
         row_m = fmaxf(row_m, bm);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // drain the V^T reads
         slot ^= 1;
         continue;
       }
@@ -342,31 +440,42 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
         grew = grew || (mc > row_m + kGrowLimit);
       }
       const float neg_m = (row_m == -__builtin_inff()) ? 0.f : -row_m;
+      // P of k-step 0 (registers 0..7) now; k-step 1 is finished inside the
+      // first PV steps, under their MFMAs.
       float pv[16];
       float lsum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 8; ++i) {
         pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, neg_m));
         lsum += pv[i];
       }
-      row_l += lsum;
       bf16x8 pf[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        u32x4 pw = {pack2_bf16<kRTNE>(pv[8 * kk + 0], pv[8 * kk + 1]), pack2_bf16<kRTNE>(pv[8 * kk + 2], pv[8 * kk + 3]),
-                    pack2_bf16<kRTNE>(pv[8 * kk + 4], pv[8 * kk + 5]), pack2_bf16<kRTNE>(pv[8 * kk + 6], pv[8 * kk + 7])};
-        pf[kk] = __builtin_bit_cast(bf16x8, pw);
+      {
+        u32x4 pw = {pack2_bf16<kRTNE>(pv[0], pv[1]), pack2_bf16<kRTNE>(pv[2], pv[3]), pack2_bf16<kRTNE>(pv[4], pv[5]),
+                    pack2_bf16<kRTNE>(pv[6], pv[7])};
+        pf[0] = __builtin_bit_cast(bf16x8, pw);
       }
+      sched_fence();
 
       // ---- O^T += V^T P^T: 16 d-tiles x 2 token k-steps ---------------------------------
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-        for (int dt = 0; dt < kDTiles; ++dt) {
-          const char* va = st + ((dt & 1) ? voff1 : voff0) + 64 * (dt >> 1) + kk * 16 * kQK;
-          const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MM_LDS i32x2*)va);
-          pv_mfma(oacc[dt], fp8x8_bf16((uint32_t)r[0], (uint32_t)r[1]), pf[kk]);
+      for (int i = 0; i < 2 * kDTiles; ++i) {
+        const int kk = i / kDTiles, dt = i % kDTiles;
+        const i32x2 r = vraw[i % kVAhead];
+        if (i + kVAhead < 2 * kDTiles)
+          vraw[i % kVAhead] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MM_LDS i32x2*)vaddr(i + kVAhead));
+        if (i < 8) {
+          pv[8 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[8 + i], c, neg_m));
+          lsum += pv[8 + i];
         }
+        if (i == 8) {
+          u32x4 pw = {pack2_bf16<kRTNE>(pv[8], pv[9]), pack2_bf16<kRTNE>(pv[10], pv[11]),
+                      pack2_bf16<kRTNE>(pv[12], pv[13]), pack2_bf16<kRTNE>(pv[14], pv[15])};
+          pf[1] = __builtin_bit_cast(bf16x8, pw);
+          row_l += lsum;
+        }
+        pv_mfma(oacc[dt], fp8x8_bf16((uint32_t)r[0], (uint32_t)r[1]), pf[kk]);
+        sched_fence();
       }
       slot ^= 1;
     }
@@ -611,7 +720,9 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   p.qrows = H * q_len;
   p.score_c = (float)((double)scale * (double)kv_scale * 1.4426950408889634);
   p.kv_scale = kv_scale;
-  const long long grid = (long long)B * p.parts * p.ngroups;
+  // Request slots per XCD for the snake deal of ranks 0..B-1 (see the kernel).
+  const int slots_per_xcd = 2 * ((B - 1) / 16) + (((B - 1) % 16) >= 8 ? 2 : 1);
+  const long long grid = (long long)mm::kNumXcds * slots_per_xcd * p.parts * p.ngroups;
   if (grid > 0x7FFFFFFFLL) return -8;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (paged)

@@ -10,7 +10,7 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.environ.get("MOONMATH_LIB", os.path.join(_HERE, "libmoonmath_gfx950.so"))
+LIB_PATH = os.environ.get("MOONMATH_LIB") or os.path.join(_HERE, "libmoonmath_gfx950.so")
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
