@@ -31,6 +31,15 @@
 //  * The 4 waves' (O, m, l) are merged through LDS, each wave finalising 4 of
 //    the 16 d-tiles. Split-KV parts > 1 write unnormalised fp32 (O, m, l)
 //    records that mla_merge_kernel combines with power-of-two weights.
+//  * Work split: the caller's parts budget P fixes a chunk size C from the
+//    batch's total context (read on the device from seq_lens), each request is
+//    cut into ceil(L / C) equal parts, and the units (request parts, longest
+//    first) are dealt in snake order over the 8 XCDs, so CTAs carry similar
+//    work whatever the length mix.
+//  * Paged gathers: each wave stages its tiles' slot indices and keeps, per
+//    tile, the first slot when the tile's tokens occupy consecutive slots (one
+//    SGPR base + per-lane offsets per DMA); any other tile is gathered row by
+//    row from per-lane slot lookups.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -56,23 +65,31 @@ constexpr int kKPairs = kQK / 32;              // 18 pairs of 16-dim k-steps (16
 constexpr int kDTiles = kLat / 32;             // 16 output d-tiles of 32
 constexpr int kMaxQLen = 8;
 constexpr int kMaxHeads = 128;
-constexpr int kIdxCap = 2048;                  // slot indices resident in LDS per sub-range
+constexpr int kTabPerWave = 512;               // tile-table entries per wave (one segment)
 // A row's running max is fixed at its first non-empty tile; later tiles may
 // exceed it by up to 2^64 (p <= 2^64, no fp32 overflow of O or l). Beyond that
 // the CTA falls back to an exact-max second pass.
 constexpr float kGrowLimit = 64.f;
 
-// LDS map (bytes): per-wave 2-slot tile rings, the slot indices of the current
-// sub-range, the rope part of Q. The merge at the end reuses the tile rings.
+// LDS map (bytes): per-wave 2-slot tile rings, per-wave tile tables (base slot
+// of each of the wave's tiles in the current segment), the rope part of Q. The
+// merge at the end reuses the tile rings.
 constexpr int kRingBytes = 2 * kTileBytes;                  // 36864 per wave
 constexpr int kStageBytes = kWaves * kRingBytes;            // 147456
-constexpr int kIdxOff = kStageBytes;
-constexpr int kQpeOff = kIdxOff + kIdxCap * 4;              // 155648
-constexpr int kLdsBytes = kQpeOff + kRowsPerCta * kRope * 2;  // 159744
-// Merge area: [wave][dt][i4][lane] x 16 B of O for 8 d-tiles, then (m, l).
+constexpr int kTabOff = kStageBytes;
+// Q dims [448, 576) (the last four k-step pairs) of the CTA's 32 rows stay in
+// LDS: 256 B per row, 16-byte chunk c of row r at chunk c ^ (r & 15).
+constexpr int kQRegPairs = 14;                 // k-step pairs whose Q lives in VGPRs
+constexpr int kQLdsDim0 = kQRegPairs * 32;     // 448
+constexpr int kQLdsRowBytes = (kQK - kQLdsDim0) * 2;  // 256
+constexpr int kQpeOff = kTabOff + kWaves * kTabPerWave * 4;  // 155648
+constexpr int kLdsBytes = kQpeOff + kRowsPerCta * kQLdsRowBytes;  // 163840
+// Staged slot indices: the last 8 KB of each wave's own ring (2048 indices).
+constexpr int kIdxStageInRing = kRingBytes - 8192;        // 28672
+// Merge area (in the tile rings): [wave][dt][i4][lane] x 16 B of O for 8 d-tiles.
 constexpr int kMergeOBytes = 8 * 4 * 64 * 16;              // 32768 per wave and half
-constexpr int kMergeMlOff = kWaves * kMergeOBytes;          // 131072
-static_assert(kMergeMlOff + kWaves * 64 * 8 <= kStageBytes, "merge area fits the rings");
+static_assert(kWaves * kMergeOBytes <= kStageBytes, "merge area fits the rings");
+static_assert(2 * 64 + 1 <= kTabPerWave, "(m, l) and the fallback flag fit a wave's tile table");
 
 // Split partial records: one per (b, part, query row): O [512] fp32, then all
 // (m, l) pairs after the last O record. kMaxRecords caps the workspace.
@@ -95,6 +112,8 @@ struct Params {
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // Two fp8 of a dword (lo or hi half) -> two bf16, exact (scale 1).
 template <bool HI>
@@ -123,32 +142,112 @@ __device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_d
   const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
 }
+// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane offset.
+__device__ __forceinline__ void dma16_sbase(const void* sbase, uint32_t voff, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
+}
+// Field `k` (16 bits) of a packed pair, extracted where it is used (volatile:
+// not hoisted, so the packed pairs are what stays live).
+__device__ __forceinline__ uint32_t u16_field(uint32_t w, int k) {
+  uint32_t r;
+  asm volatile("v_bfe_u32 %0, %1, %2, 16" : "=v"(r) : "v"(w), "i"(16 * k));
+  return r;
+}
 
-// Request holding length rank `rank` (0 = longest) among B requests, in an
-// approximate longest-first order: 16 linear length buckets, longest bucket
-// first, request index order inside a bucket. Wave-uniform; every wave of a
-// CTA computes it independently from the same seq_lens.
-__device__ __forceinline__ int request_of_rank(const int* seq_lens, int B, int rank, int lane) {
-  int maxl = 0;
+// ---- split plan ------------------------------------------------------------------------
+// The caller's `parts` P is a budget: with sumL the total context of the batch,
+// every request is cut into chunks of C tokens,
+//   C = max(512, roundup32(ceil(sumL / (B (P - 1)))))   (P > 1),
+// request b getting nparts_b = ceil(L_b / C) parts (at least 1). Because
+// ceil(L/C) < L/C + 1, sum_b nparts_b < sumL / C + B <= B P: the partial records
+// always fit the B * P * qrows workspace. Parts of one request have equal token
+// counts except the last, so CTAs carry similar work whatever the lengths.
+constexpr int kMinChunk = 512;
+// The paged plan keeps three B-entry tables in one wave's tile ring.
+constexpr int kMaxPagedB = kRingBytes / 12;  // 3072
+
+__device__ __forceinline__ int chunk_tokens(long long sumL, int B, int P) {
+  if (P <= 1) return 0x7FFFFFE0;
+  long long c = (sumL + (long long)B * (P - 1) - 1) / ((long long)B * (P - 1));
+  c = (c + kTileTok - 1) / kTileTok * kTileTok;
+  if (c < kMinChunk) c = kMinChunk;
+  return c > 0x7FFFFFE0 ? 0x7FFFFFE0 : (int)c;
+}
+__device__ __forceinline__ int nparts_of(int L, int C) { return L <= C ? 1 : (L + C - 1) / C; }
+// Tokens per part of a request of L tokens in np parts: equal shares rounded up
+// to whole tiles (the last part takes the remainder).
+__device__ __forceinline__ int part_tokens(int L, int np) {
+  const int t = (L + np - 1) / np;
+  return (t + kTileTok - 1) / kTileTok * kTileTok;
+}
+
+// Wave64 reductions and inclusive scan on DPP row shifts / broadcasts (no LDS).
+__device__ __forceinline__ int wave_incl_scan(int v);
+__device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
+__device__ __forceinline__ int wave_max_i(int v) {
+  // Invalid DPP sources return `old` = the lane's own value (neutral for max).
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+struct Unit {
+  int b;       // request
+  int part;    // part within the request
+  int nparts;  // parts of the request
+  int rec0;    // record part index of the request's part 0 (request-index order)
+  int ptok;    // tokens per part of this request
+  int units;   // total units (request parts) in the batch
+};
+
+// Unit `u` of the batch in longest-first order: requests sorted into 16 linear
+// buckets of their part size (largest first, request index inside a bucket),
+// each request's parts consecutive. Wave-uniform; every wave of a CTA computes
+// it on its own, using `scratch` (12 * B bytes of this wave's LDS).
+__device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int lane, int* scratch) {
+  int* lens = scratch;            // [B] lengths, then part sizes
+  int* req_at = scratch + B;      // [B] request at each position
+  int* np_at = scratch + 2 * B;   // [B] parts of the request at each position
+  long long suml = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const int l = (c0 + lane < B) ? seq_lens[c0 + lane] : 0;
-    int m = l;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off));
-    maxl = max(maxl, m);
+    if (c0 + lane < B) lens[c0 + lane] = l;
+    suml += wave_sum_i(l);  // per-chunk sums stay below 2^31 for lengths < 2^25
   }
-  maxl = __builtin_amdgcn_readfirstlane(maxl);
-  auto bucket_of = [&](int l) {  // 0 = longest lengths
-    const long long q = (long long)l * 16 / ((long long)maxl + 1);
+  const int C = chunk_tokens(suml, B, P);
+  int maxp = 0;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const bool valid = c0 + lane < B;
+    const int l = valid ? lens[c0 + lane] : 0;
+    const int pt = valid ? part_tokens(l, nparts_of(l, C)) : 0;
+    maxp = max(maxp, wave_max_i(pt));
+  }
+  maxp = __builtin_amdgcn_readfirstlane(maxp);
+  auto bucket_of = [&](int pt) {  // 0 = largest parts
+    const long long q = (long long)pt * 16 / ((long long)maxp + 1);
     return 15 - (int)q;
   };
-  // Bucket sizes over all requests.
   int start[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) start[k] = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const bool valid = c0 + lane < B;
-    const int bk = valid ? bucket_of(seq_lens[c0 + lane]) : -1;
+    const int l = valid ? lens[c0 + lane] : 0;
+    const int bk = valid ? bucket_of(part_tokens(l, nparts_of(l, C))) : -1;
 #pragma unroll
     for (int k = 0; k < 16; ++k) start[k] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bk == k));
   }
@@ -159,22 +258,60 @@ __device__ __forceinline__ int request_of_rank(const int* seq_lens, int B, int r
     start[k] = acc;
     acc += c;
   }
-  // Position of every request; the one at `rank` wins.
   const unsigned long long lt = (1ull << lane) - 1ull;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const bool valid = c0 + lane < B;
-    const int bk = valid ? bucket_of(seq_lens[c0 + lane]) : -1;
-    int pos = -1;
+    const int l = valid ? lens[c0 + lane] : 0;
+    const int np = nparts_of(l, C);
+    const int bk = valid ? bucket_of(part_tokens(l, np)) : -1;
+    int pos = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const unsigned long long m = __builtin_amdgcn_ballot_w64(bk == k);
       if (bk == k) pos = start[k] + __builtin_popcountll(m & lt);
       start[k] += __builtin_popcountll(m);
     }
-    const unsigned long long hit = __builtin_amdgcn_ballot_w64(valid && pos == rank);
-    if (hit) return c0 + (int)__builtin_ctzll(hit);
+    if (valid) {
+      req_at[pos] = c0 + lane;
+      np_at[pos] = np;
+    }
   }
-  return 0;  // unreachable for rank < B
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  Unit r{0, 0, 1, 0, kTileTok, 0};
+  int run = 0;  // units before this chunk of positions
+  bool found = false;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const bool valid = c0 + lane < B;
+    const int np = valid ? np_at[c0 + lane] : 0;
+    const int inc = wave_incl_scan(np);
+    const int excl = run + inc - np;
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(valid && u >= excl && u < excl + np);
+    if (!found && hit) {
+      const int hl = (int)__builtin_ctzll(hit);
+      r.b = __builtin_amdgcn_readlane(req_at[c0 + lane], hl);
+      r.part = u - __builtin_amdgcn_readlane(excl, hl);
+      r.nparts = __builtin_amdgcn_readlane(np, hl);
+      found = true;
+    }
+    run += __builtin_amdgcn_readlane(inc, 63);
+  }
+  r.units = run;
+  r.ptok = part_tokens(lens[r.b], r.nparts);
+  // Record offset: parts of the requests before b, in request-index order.
+  int rec0 = 0;
+  for (int c0 = 0; c0 < B; c0 += 64) {
+    const int idx = c0 + lane;
+    rec0 += wave_sum_i(idx < B && idx < r.b ? nparts_of(lens[idx], C) : 0);
+  }
+  r.rec0 = rec0;
+  return r;
+}
+
+// 4-byte global -> LDS DMA (lane l's dword lands at lds_dst + 4*l), counted by
+// the kernel itself like dma16_opaque.
+__device__ __forceinline__ void dma4_opaque(const void* gsrc, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dword %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
 }
 
 // Staging layout of one tile: token t's 576-byte row at t*576, its 16-byte
@@ -186,7 +323,7 @@ __device__ __forceinline__ int swz(int t) { return (t >> 2) & 3; }
 template <bool PAGED>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
-  int* idx_lds = reinterpret_cast<int*>(lds + kIdxOff);
+  int* tab = reinterpret_cast<int*>(lds + kTabOff) + (threadIdx.x >> 6) * kTabPerWave;  // this wave's tile table
   char* qpe_lds = lds + kQpeOff;
 
   const int tid = threadIdx.x;
@@ -198,20 +335,26 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
 
   // ---- work item ----------------------------------------------------------------------
   // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8) and in
-  // blockIdx order within an XCD. Request slots are dealt to XCDs in snake order
-  // of decreasing length (XCD x takes length ranks x, 15-x, 16+x, 31-x, ...), so
-  // every XCD gets a similar share, the E = parts * ngroups CTAs of a request
-  // run on one XCD (its KV is shared through that L2) and each XCD starts its
-  // longest requests first.
-  const int E = p.parts * p.ngroups;
+  // blockIdx order within an XCD. Units (request parts, longest first) are dealt
+  // to XCDs in snake order (XCD x takes units x, 15-x, 16+x, 31-x, ...) so every
+  // XCD gets a similar share and starts with its longest units; the ngroups CTAs
+  // of a unit run on one XCD (its KV is shared through that L2).
   const int xcd = blockIdx.x % kNumXcds;
   const int k_in_xcd = blockIdx.x / kNumXcds;
-  const int tslot = k_in_xcd / E, e = k_in_xcd % E;
-  const int rank = 16 * (tslot >> 1) + ((tslot & 1) ? 15 - xcd : xcd);
-  if (rank >= p.B) return;  // padding CTA (whole CTA, before any barrier)
-  const int part = e / p.ngroups;
-  const int grp = e % p.ngroups;
-  const int b = PAGED ? request_of_rank(p.seq_lens, p.B, rank, lane) : rank;
+  const int uslot = k_in_xcd / p.ngroups;
+  const int grp = k_in_xcd % p.ngroups;
+  const int u = 16 * (uslot >> 1) + ((uslot & 1) ? 15 - xcd : xcd);
+  Unit un;
+  if constexpr (PAGED) {
+    un = plan_unit_paged(p.seq_lens, p.B, p.parts, u, lane, reinterpret_cast<int*>(wring));
+  } else {
+    const int C = chunk_tokens((long long)p.B * p.S_fixed, p.B, p.parts);
+    const int np = nparts_of(p.S_fixed, C);
+    un = Unit{u / np, u % np, np, (u / np) * np, part_tokens(p.S_fixed, np), p.B * np};
+  }
+  if (u >= un.units) return;  // padding CTA (whole CTA, before any barrier)
+  const int b = un.b;
+  const int part = un.part;
   int qb = b;
   if (p.rows) {
     qb = p.rows[b];
@@ -219,10 +362,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   }
   const int S = PAGED ? p.seq_lens[b] : p.S_fixed;
   const int slot0 = PAGED ? p.kv_indptr[b] : 0;
-  // Proportional split: each part covers ceil(S / parts) tokens rounded to tiles.
-  const int part_tok = ((S + p.parts * kTileTok - 1) / (p.parts * kTileTok)) * kTileTok;
-  const int kv_lo = part * part_tok;
-  const int kv_hi = (kv_lo + part_tok < S) ? kv_lo + part_tok : S;
+  const long long lo64 = (long long)part * un.ptok;
+  const int kv_lo = lo64 < S ? (int)lo64 : S;
+  const int kv_hi = (lo64 + un.ptok < S) ? (int)(lo64 + un.ptok) : S;
 
   // ---- query row of this lane ----------------------------------------------------
   const int qrow = grp * kRowsPerCta + n;  // row within (t, h)
@@ -232,29 +374,61 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   const int lim = S - (p.q_len - 1 - t_pos);  // tokens >= lim are masked for this row
   const long long qoff = (long long)qb * p.qrows + qr;  // row index into [B, q_len, H]
 
-  // Q fragments (B operand of S^T = K Q^T). k-step pair s covers dims
-  // 32s + 16g .. +16 of lane half g: the first 8 feed k-step 2s, the next 8 k-step
-  // 2s+1 (the same dims the K fragment of that lane half holds).
-  bf16x8 qf[2 * (kKPairs - 2)];
+  // Slot indices of this wave's tiles of a segment (32 per tile, two tiles per
+  // 4-byte DMA, at most 64 tiles per call) into the last 8 KB of this wave's
+  // ring: tile-major, 128 B per tile. Lanes past the segment re-read its last
+  // index.
+  auto stage_idx = [&](int seg_lo, int seg_hi, int i0, int nb) {
+    if constexpr (PAGED) {
+      for (int q = 0; q < (nb + 1) / 2; ++q) {
+        const int i = i0 + 2 * q + g;
+        int tok = seg_lo + kTileTok * (wave + kWaves * i) + n;
+        tok = tok < seg_hi ? tok : seg_hi - 1;
+        dma4_opaque(p.kv_indices + slot0 + tok, wring + kIdxStageInRing + 256 * q);
+      }
+    }
+  };
+  auto seg_end = [&](int seg_lo) {
+    const long long e = (long long)seg_lo + kWaves * kTabPerWave * kTileTok;
+    return e < kv_hi ? (int)e : kv_hi;
+  };
+  auto my_tiles = [&](int seg_lo, int seg_hi) {
+    const int ntiles = (seg_hi - seg_lo + kTileTok - 1) / kTileTok;
+    return (wave < ntiles) ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+  };
+
+  // Q fragments (B operand of S^T = K Q^T on v_mfma_f32_32x32x16_bf16; A = K
+  // widened exactly from the staged fp8 tile). k-step pair s covers dims
+  // 32s + 16g .. +16 of lane half g: the first 8 feed k-step 2s, the next 8
+  // k-step 2s+1 (the same dims the K fragment of that lane half holds).
+  if (kv_lo < kv_hi) {  // index batch of the first segment, with the Q loads
+    const int nm = my_tiles(kv_lo, seg_end(kv_lo));
+    stage_idx(kv_lo, seg_end(kv_lo), 0, nm < 64 ? nm : 64);
+  }
+  bool idx_prestaged = true;
+  bf16x8 qf[2 * kQRegPairs];
 #pragma unroll
-  for (int s = 0; s < kKPairs - 2; ++s) {
+  for (int s = 0; s < kQRegPairs; ++s) {
     const uint16_t* src = p.q_lat + qoff * kLat + s * 32 + g * 16;
     qf[2 * s] = *reinterpret_cast<const bf16x8*>(src);
     qf[2 * s + 1] = *reinterpret_cast<const bf16x8*>(src + 8);
   }
-  // Rope part of Q: 32 rows x 64 bf16 in LDS (row n at n * 128 B).
-  if (tid < kRowsPerCta * 8) {
-    const int r = tid >> 3, c = tid & 7;
+  // Q dims [448, 576): 32 rows x 16 chunks of 8 bf16 (chunks 0..7 from q_lat,
+  // 8..15 = the rope part from q_pe) into LDS.
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int id = tid + it * kThreads;  // 512 chunks
+    const int r = id >> 4, c = id & 15;
     const int rr = grp * kRowsPerCta + r;
     const long long ro = (long long)qb * p.qrows + (rr < p.qrows ? rr : p.qrows - 1);
-    *reinterpret_cast<bf16x8*>(qpe_lds + r * 128 + c * 16) =
-        *reinterpret_cast<const bf16x8*>(p.q_pe + ro * kRope + c * 8);
+    const uint16_t* src = (c < 8) ? p.q_lat + ro * kLat + kQLdsDim0 + c * 8 : p.q_pe + ro * kRope + (c - 8) * 8;
+    *reinterpret_cast<bf16x8*>(qpe_lds + r * kQLdsRowBytes + 16 * (c ^ (r & 15))) = *reinterpret_cast<const bf16x8*>(src);
   }
 
-  // Retire the Q loads here, visibly to the compiler (vmcnt 0, expcnt/lgkmcnt
-  // untouched): the tile DMAs are invisible to its wait-count model, so a Q
-  // wait left to the loop would become a per-tile vmcnt countdown that also
-  // waits for the prefetched tile.
+  // Retire the Q and index loads here, visibly to the compiler (vmcnt 0,
+  // expcnt/lgkmcnt untouched): the tile DMAs are invisible to its wait-count
+  // model, so a wait left to the loop would become a per-tile vmcnt countdown
+  // that also waits for the prefetched tile.
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // ---- per-lane constant offsets inside a staged tile -------------------------------
@@ -273,13 +447,17 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   // per row, 9 instructions cover exactly 16 token rows, so the lane pattern of
   // k and k+9 is the same 16 rows later. dma_off[k9] = tg*576 + 16*c for the
   // piece slot this lane fills (tg = token within the 16-row group).
-  int dma_off[9];
+  // Offsets are < 2^14: two per VGPR (dma_pk[k9 / 2], low half for even k9).
+  uint32_t dma_pk[5];
 #pragma unroll
   for (int k9 = 0; k9 < 9; ++k9) {
     const int pc = 64 * k9 + lane;
     const int tg = pc / 36, cs = pc % 36;
-    dma_off[k9] = tg * kQK + 16 * (cs ^ swz(tg));
+    const uint32_t off = tg * kQK + 16 * (cs ^ swz(tg));
+    dma_pk[k9 / 2] = (k9 & 1) ? (dma_pk[k9 / 2] | (off << 16)) : off;
   }
+  auto dma_off = [&](int k9) -> int { return (int)((dma_pk[k9 / 2] >> (16 * (k9 & 1))) & 0xFFFFu); };
+  auto dma_offv = [&](int k9) { return u16_field(dma_pk[k9 / 2], k9 & 1); };
 
   f32x16 oacc[kDTiles];
 #pragma unroll
@@ -293,63 +471,85 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   // largest masked score only (row_m then holds the raw score max).
   auto sweep = [&](auto max_only_tag) {
   constexpr bool kMaxOnly = decltype(max_only_tag)::value;
-  for (int sub_lo = kv_lo; sub_lo < kv_hi; sub_lo += kIdxCap) {
-    const int sub_hi = (sub_lo + kIdxCap < kv_hi) ? sub_lo + kIdxCap : kv_hi;
-    const int ntiles = (sub_hi - sub_lo + kTileTok - 1) / kTileTok;
+  // Segments of up to kTabPerWave tiles per wave (one for any part up to 64K tokens).
+  for (int seg_lo = kv_lo; seg_lo < kv_hi; seg_lo += kWaves * kTabPerWave * kTileTok) {
+    const int seg_hi = seg_end(seg_lo);
+    const int ntiles = (seg_hi - seg_lo + kTileTok - 1) / kTileTok;
+    const int nmine = my_tiles(seg_lo, seg_hi);  // tiles wave, wave+4, ...
     if constexpr (PAGED) {
-      lds_reads_done_barrier_vm0();  // every wave is done with the previous indices
-      for (int i = tid; i < sub_hi - sub_lo; i += kThreads) idx_lds[i] = p.kv_indices[slot0 + sub_lo + i];
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    } else {
-      if (sub_lo == kv_lo) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // qpe_lds
-    }
-    const int eff = lim < sub_hi ? lim : sub_hi;  // this row's token limit in the sub-range
-
-    // Gather plan of tile j (tokens sub_lo + 32j ..). Fast path: the 32 rows are
-    // consecutive slots (always for the contiguous layout, and for paged tiles
-    // inside one page): DMA k reads base + (k/9)*16 rows + dma_off[k%9]. Slow
-    // path: every lane looks its row up, with tokens past sub_hi clamped to the
-    // last valid one (their scores are masked).
-    auto tile_fast = [&](int j, const uint8_t*& base) -> bool {
-      const int tok0 = sub_lo + j * kTileTok;
-      bool fast = tok0 + kTileTok <= sub_hi;
-      long long row0 = (long long)b * p.S_fixed + tok0;
-      if constexpr (PAGED) {
-        if (fast) {
-          const int i0 = __builtin_amdgcn_readfirstlane(idx_lds[tok0 - sub_lo]);
-          const int mine = idx_lds[tok0 - sub_lo + n];
-          fast = __builtin_amdgcn_ballot_w64(mine == i0 + n) == ~0ull;
-          row0 = i0;
+      // Tile table of this wave's tiles: the slot indices of each tile (32 per
+      // tile, two tiles per 4-byte DMA) are staged in this wave's ring, then
+      // tab[i] = slot of the tile's first token if its valid tokens occupy
+      // consecutive slots (the gather is one base + lane offsets), else -1.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring is free (previous segment drained)
+      for (int i0 = 0; i0 < nmine; i0 += 64) {
+        const int nb = (nmine - i0 < 64) ? nmine - i0 : 64;
+        if (!(idx_prestaged && seg_lo == kv_lo && i0 == 0)) stage_idx(seg_lo, seg_hi, i0, nb);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        for (int q = 0; q < (nb + 1) / 2; ++q) {
+          const int i = i0 + 2 * q + g;
+          const int v = *reinterpret_cast<const int*>(wring + kIdxStageInRing + 256 * q + 4 * lane);
+          const int first = __shfl(v, 32 * g);
+          const int tok = seg_lo + kTileTok * (wave + kWaves * i) + n;
+          const unsigned long long bal = __builtin_amdgcn_ballot_w64(tok >= seg_hi || v == first + n);
+          const bool contiguous = ((bal >> (32 * g)) & 0xffffffffull) == 0xffffffffull;
+          if (n == 0 && i < nmine) tab[i] = contiguous ? first : -1;
         }
       }
-      base = p.kv + row0 * kQK;
-      return fast;
+    }
+    idx_prestaged = false;  // a later sweep re-stages its indices
+    if (seg_lo == kv_lo) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // qpe_lds
+    const int eff = lim < seg_hi ? lim : seg_hi;  // this row's token limit in the segment
+
+    // Gather of tile j (tokens seg_lo + 32j ..), j = wave + 4i. Fast path: the
+    // tile's rows are consecutive slots (always for the contiguous layout, and
+    // for paged tiles inside one page): DMA k reads base + (k/9)*16 rows +
+    // dma_off[k%9], with rows past the valid ones clamped to the last valid row
+    // in a partial tile. Slow path: every lane looks its row up.
+    auto tile_base = [&](int j, const uint8_t*& base) -> bool {
+      const int tok0 = seg_lo + j * kTileTok;
+      if constexpr (PAGED) {
+        const int s0 = __builtin_amdgcn_readfirstlane(tab[j / kWaves]);
+        base = p.kv + (long long)s0 * kQK;
+        return s0 >= 0;
+      } else {
+        base = p.kv + ((long long)b * p.S_fixed + tok0) * kQK;
+        return true;
+      }
     };
-    auto issue_slow = [&](int j, const char* dst) {
-      const int tok0 = sub_lo + j * kTileTok;
+    auto issue_partial = [&](int j, const uint8_t* base, const char* dst) {
+      const int nvalid = seg_hi - (seg_lo + j * kTileTok);
 #pragma unroll 1
       for (int k = 0; k < kDmaPerTile; ++k) {
-        const int k9 = k % 9;
-        const int pc = 64 * k9 + lane;
-        const int tg = pc / 36, cs = pc - 36 * (pc / 36);
-        int tok = tok0 + (k / 9) * 16 + tg;
-        tok = tok < sub_hi ? tok : sub_hi - 1;
-        long long row;
-        if constexpr (PAGED) {
-          row = idx_lds[tok - sub_lo];
-        } else {
-          row = (long long)b * p.S_fixed + tok;
-        }
-        dma16_opaque(p.kv + row * kQK + 16 * (cs ^ swz(tg)), dst + 1024 * k);
+        const int o = dma_off(k % 9);
+        const int tg = (o * 7282) >> 22;  // o / 576 for o < 9216
+        int t = (k / 9) * 16 + tg;
+        t = t < nvalid ? t : nvalid - 1;
+        dma16_opaque(base + t * kQK + (o - tg * kQK), dst + 1024 * k);
+      }
+    };
+    auto issue_slow = [&](int j, const char* dst) {
+      const int tok0 = seg_lo + j * kTileTok;
+      int tk = tok0 + n;
+      tk = tk < seg_hi ? tk : seg_hi - 1;
+      const int myrow = p.kv_indices[slot0 + tk];  // lane n: slot of token tok0 + n
+#pragma unroll 1
+      for (int k = 0; k < kDmaPerTile; ++k) {
+        const int o = dma_off(k % 9);
+        const int tg = (o * 7282) >> 22;
+        const int row = __shfl(myrow, (k / 9) * 16 + tg);
+        dma16_opaque(p.kv + (long long)row * kQK + (o - tg * kQK), dst + 1024 * k);
       }
     };
     auto issue_tile = [&](int j, const char* dst) {
       const uint8_t* base;
-      if (tile_fast(j, base)) {
-#pragma unroll
-        for (int k = 0; k < kDmaPerTile; ++k) dma16_opaque(base + (k / 9) * 16 * kQK + dma_off[k % 9], dst + 1024 * k);
-      } else {
+      if (!tile_base(j, base)) {
         issue_slow(j, dst);
+      } else if (seg_lo + (j + 1) * kTileTok > seg_hi) {
+        issue_partial(j, base, dst);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kDmaPerTile; ++k) dma16_sbase(base + (k / 9) * 16 * kQK, dma_offv(k % 9), dst + 1024 * k);
       }
     };
 
@@ -359,48 +559,62 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile has landed
       const char* st = wring + slot * kTileBytes;
       const char* nst = wring + (slot ^ 1) * kTileBytes;
-      const int tok0 = sub_lo + j * kTileTok;
-      // Next tile of this wave: a fast-path gather is spread over the 18 QK
-      // steps below (one DMA each); a slow-path gather is issued here.
+      const int tok0 = seg_lo + j * kTileTok;
+      // Next tile of this wave: a full fast-path gather is spread over the 18
+      // QK steps below (one DMA each); any other gather is issued here.
       const uint8_t* nbase = nullptr;
       bool ndma = false;
       if (j + kWaves < ntiles) {
-        ndma = tile_fast(j + kWaves, nbase);
-        if (!ndma) issue_slow(j + kWaves, nst);
+        const bool full = seg_lo + (j + kWaves + 1) * kTileTok <= seg_hi;
+        ndma = full && tile_base(j + kWaves, nbase);
+        if (!ndma) issue_tile(j + kWaves, nst);
       }
+      ndma = __builtin_amdgcn_readfirstlane((int)ndma) != 0;
 
       // ---- S^T = K Q^T: 18 k-step pairs, two accumulator chains ------------------------
-      // K pieces are read kKAhead pairs ahead of their conversion; sched_fence()
-      // keeps each step's [DMA, read ahead, convert, 2 MFMA] order.
+      // K pieces are read kKAhead pairs ahead of their conversion; each step
+      // also issues one DMA of the next tile. One straight-line body per DMA
+      // mode, so no branch splits the steps; sched_fence() keeps each step's
+      // [DMA, read ahead, convert, 2 MFMA] order.
       constexpr int kKAhead = 4;
       auto kaddr = [&](int s) { return st + ((s & 1) ? koff1 : koff0) + 64 * (s >> 1); };
-      u32x4 kraw[kKAhead];
+      auto qk = [&](auto with_dma) {
+        u32x4 kraw[kKAhead];
 #pragma unroll
-      for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(s));
-      bf16x8 qpe[4];
-      f32x16 s0 = f32x16{}, s1 = f32x16{};
+        for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(s));
+        bf16x8 qpa, qpb;  // LDS-resident Q of the next pair, read one step ahead
+        f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
-      for (int s = 0; s < kKPairs; ++s) {
-        if (ndma) dma16_opaque(nbase + (s / 9) * 16 * kQK + dma_off[s % 9], nst + 1024 * s);
-        const u32x4 raw = kraw[s % kKAhead];
-        if (s + kKAhead < kKPairs) kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(s + kKAhead));
-        if (s == kKPairs - 2 - kKAhead) {  // rope part of Q for the last two pairs
-          const char* qp = qpe_lds + n * 128 + g * 32;
-          qpe[0] = *reinterpret_cast<const bf16x8*>(qp);
-          qpe[1] = *reinterpret_cast<const bf16x8*>(qp + 16);
-          qpe[2] = *reinterpret_cast<const bf16x8*>(qp + 64);
-          qpe[3] = *reinterpret_cast<const bf16x8*>(qp + 80);
+        for (int s = 0; s < kKPairs; ++s) {
+          if constexpr (decltype(with_dma)::value)
+            dma16_sbase(nbase + (s / 9) * 16 * kQK, dma_offv(s % 9), nst + 1024 * s);
+          const u32x4 raw = kraw[s % kKAhead];
+          if (s + kKAhead < kKPairs) kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(s + kKAhead));
+          bf16x8 qa, qb2;
+          if (s >= kQRegPairs) {
+            qa = qpa;
+            qb2 = qpb;
+          } else {
+            qa = qf[2 * s];
+            qb2 = qf[2 * s + 1];
+          }
+          if (s + 1 >= kQRegPairs && s + 1 < kKPairs) {
+            const char* qrow_p = qpe_lds + n * kQLdsRowBytes;
+            const int c0 = 4 * (s + 1 - kQRegPairs) + 2 * g;  // chunk of dims 32(s+1) + 16g
+            qpa = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * (c0 ^ (n & 15)));
+            qpb = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * ((c0 + 1) ^ (n & 15)));
+          }
+          const bf16x8 ka = fp8x8_bf16(raw[0], raw[1]);
+          const bf16x8 kb = fp8x8_bf16(raw[2], raw[3]);
+          s0 = mfma32(ka, qa, s0);
+          s1 = mfma32(kb, qb2, s1);
+          sched_fence();
         }
-        const bf16x8 ka = fp8x8_bf16(raw[0], raw[1]);
-        const bf16x8 kb = fp8x8_bf16(raw[2], raw[3]);
-        const bf16x8 qa = (s < kKPairs - 2) ? qf[2 * s] : qpe[2 * (s - (kKPairs - 2))];
-        const bf16x8 qb2 = (s < kKPairs - 2) ? qf[2 * s + 1] : qpe[2 * (s - (kKPairs - 2)) + 1];
-        s0 = mfma32(ka, qa, s0);
-        s1 = mfma32(kb, qb2, s1);
-        sched_fence();
-      }
+        return s0 + s1;
+      };
+      const f32x16 sacc = ndma ? qk(std::true_type{}) : qk(std::false_type{});
       // V^T transpose reads for the first PV steps go out before the softmax.
-      constexpr int kVAhead = 8;
+      constexpr int kVAhead = 6;
       auto vaddr = [&](int i) {
         const int kk = i / kDTiles, dt = i % kDTiles;
         return st + ((dt & 1) ? voff1 : voff0) + 64 * (dt >> 1) + kk * 16 * kQK;
@@ -412,7 +626,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
       // Lane (n, g), register i: token tok0 + 8(i/4) + 4g + i%4 of query row n.
       float sv[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sv[i] = s0[i] + s1[i];
+      for (int i = 0; i < 16; ++i) sv[i] = sacc[i];
       const int rel = eff - tok0 - 4 * g;  // register i is valid iff 8(i/4) + i%4 < rel
       if (__builtin_amdgcn_ballot_w64(rel < 32)) {  // the window or the range ends in this tile
 #pragma unroll
@@ -482,43 +696,51 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   }
   };
 
+  // Each wave posts its (m, l) per lane and its fallback flag into its own
+  // tile-table area (no other wave touches it), then one barrier.
+  auto post_ml = [&]() {
+    mfma_result_fence();
+    float* mine = reinterpret_cast<float*>(tab);
+    mine[2 * lane] = row_m;
+    mine[2 * lane + 1] = row_l;
+    if (lane == 0) reinterpret_cast<int*>(tab)[128] = __builtin_amdgcn_ballot_w64(grew) != 0;
+    lds_reads_done_barrier_vm0();
+  };
+  auto ml_of = [&](int v, int i) {
+    return reinterpret_cast<const float*>(lds + kTabOff)[v * kTabPerWave + 2 * lane + i];
+  };
+  auto retry_of = [&]() {
+    const int* base = reinterpret_cast<const int*>(lds + kTabOff);
+    return (base[128] | base[kTabPerWave + 128] | base[2 * kTabPerWave + 128] | base[3 * kTabPerWave + 128]) != 0;
+  };
   sweep(std::false_type{});
+  post_ml();
   // Fallback (never taken unless some row's scores rise more than 2^64 above
   // its first tile): every wave redoes its tiles with the exact row max. The
   // decision is CTA-uniform because the sweeps hold CTA barriers.
-  {
-    int* flags = reinterpret_cast<int*>(lds + kMergeMlOff);
-    lds_reads_done_barrier_vm0();
-    if (lane == 0) flags[wave] = __builtin_amdgcn_ballot_w64(grew) != 0;
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const bool retry = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
-    if (retry) {
-      row_m = -__builtin_inff();
-      sweep(std::true_type{});
-      row_m = __builtin_ceilf(row_m * c);
-      row_l = 0.f;
-      mfma_result_fence();
+  if (retry_of()) {
+    asm volatile("s_barrier" ::: "memory");  // every wave has read the flags
+    row_m = -__builtin_inff();
+    sweep(std::true_type{});
+    row_m = __builtin_ceilf(row_m * c);
+    row_l = 0.f;
+    grew = false;
+    mfma_result_fence();
 #pragma unroll
-      for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = f32x16{};
-      sweep(std::false_type{});
-    }
+    for (int dt = 0; dt < kDTiles; ++dt) oacc[dt] = f32x16{};
+    sweep(std::false_type{});
+    post_ml();
   }
 
   // ---- merge the 4 waves' (O, m, l) through LDS ---------------------------------------
   // Rows of lanes n and n+32 are the same query row: m agrees, l is summed at the end.
-  mfma_result_fence();
-  lds_reads_done_barrier_vm0();  // every wave is done with its ring
-  float* mlarea = reinterpret_cast<float*>(lds + kMergeMlOff);
-  mlarea[(wave * 64 + lane) * 2] = row_m;
-  mlarea[(wave * 64 + lane) * 2 + 1] = row_l;
   // Lane weights of the 4 waves, exact powers of two.
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   float mw[kWaves], lw[kWaves];
   float M = -__builtin_inff();
 #pragma unroll
   for (int v = 0; v < kWaves; ++v) {
-    mw[v] = mlarea[(v * 64 + lane) * 2];
-    lw[v] = mlarea[(v * 64 + lane) * 2 + 1];
+    mw[v] = ml_of(v, 0);
+    lw[v] = ml_of(v, 1);
     M = fmaxf(M, mw[v]);
   }
   float wt[kWaves];
@@ -530,9 +752,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     L = __builtin_fmaf(wt[v], lw[v], L);
   }
   L = xor32_sum(L);  // whole-row sum (lanes n and n+32)
-  const bool split = p.parts > 1;
+  const bool split = un.nparts > 1;
   const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
-  const size_t rec = ((size_t)b * p.parts + part) * p.qrows + qrow;
+  const size_t rec = ((size_t)un.rec0 + part) * p.qrows + qrow;
   uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow) * kLat;
   float* prow = p.ws + rec * kLat;
 
@@ -586,6 +808,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     pml[0] = M;
     pml[1] = L;
   }
+  if (p.parts > 1 && part == 0 && grp == 0 && tid == 0) {
+    // Per-request (parts, first record) table for the merge kernel.
+    int* tbl = reinterpret_cast<int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
+    tbl[2 * b] = un.nparts;
+    tbl[2 * b + 1] = un.rec0;
+  }
 }
 
 // Merge: one thread = 4 output dims of one (b, query row).
@@ -604,15 +832,19 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
     qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
   }
   const float* ml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat;
+  const int* tbl = reinterpret_cast<const int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
+  const int nparts = tbl[2 * b];
+  const int rec0 = tbl[2 * b + 1];
+  if (nparts <= 1) return;  // the decode kernel wrote this request's output
   float M = -__builtin_inff();
-  for (int j = 0; j < p.parts; ++j) {
-    const size_t rec = ((size_t)b * p.parts + j) * p.qrows + qrow;
+  for (int j = 0; j < nparts; ++j) {
+    const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
     M = fmaxf(M, ml[rec * 2]);
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  for (int j = 0; j < p.parts; ++j) {
-    const size_t rec = ((size_t)b * p.parts + j) * p.qrows + qrow;
+  for (int j = 0; j < nparts; ++j) {
+    const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
     const float m_p = ml[rec * 2];
     const float l_p = ml[rec * 2 + 1];
     const float diff = m_p - M;  // integer-valued or -inf, <= 0
@@ -655,7 +887,6 @@ using namespace mm::mla;
 
 constexpr int kQRowsPerCta = kRowsPerCta;  // 32
 constexpr int kNumCUs = 256;
-constexpr int kCtasPerCu = 1;
 constexpr int kMaxParts = 64;
 
 int ngroups_for(int H, int q_len) { return (H * q_len + kQRowsPerCta - 1) / kQRowsPerCta; }
@@ -668,15 +899,20 @@ int max_parts_for(int B, int H, int q_len) {
   return m < 1 ? 1 : (int)m;
 }
 
-// Split planner: enough CTAs for ~2 rounds over the CUs (ragged lengths balance
-// across rounds), at least 4 tiles per wave in a part, within the record workspace.
+// Split planner. The kernel cuts requests into equal chunks so that the batch
+// has about B * (parts - 1) + B/2 units (request parts); aim at ~1.5 rounds of
+// CTAs over the CUs for wide query rows (4+ row groups) and one round for
+// narrow ones (per-CTA set-up dominates short CTAs), within the record cap.
 int plan_parts(int B, int H, int max_seq_len, int q_len) {
   if (B < 1) B = 1;
   if (q_len < 1) q_len = 1;
-  const int tiles = (max_seq_len + kTileTok - 1) / kTileTok;
-  const int ctas_per_part = B * ngroups_for(H, q_len);
-  int p = (2 * kNumCUs * kCtasPerCu + ctas_per_part - 1) / ctas_per_part;
-  if (p > tiles / 16) p = tiles / 16;
+  const int ng = ngroups_for(H, q_len);
+  // Units ~ B * (p - 1) + B / 2 (see the kernel's chunking).
+  const int ctas = ng >= 4 ? (3 * kNumCUs) / 2 : kNumCUs;
+  const int units = ctas / ng;
+  int p = units > B / 2 ? 1 + (units - B / 2) / B : 1;
+  const int by_len = 1 + max_seq_len / 512;  // chunks are at least 512 tokens
+  if (p > by_len) p = by_len;
   const int cap = max_parts_for(B, H, q_len);
   if (p > cap) p = cap;
   return p < 1 ? 1 : p;
@@ -697,6 +933,7 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   if (lat_dim != kLat || rope_dim != kRope) return -2;
   if (H < 1 || H > kMaxHeads) return -3;
   if (q_len < 1 || q_len > kMaxQLen || B < 1) return -4;
+  if (paged && B > kMaxPagedB) return -4;
   if (!q_lat || !q_pe || !kv || !o_lat) return -6;
   if (paged && (!seq_lens || !kv_indices || !kv_indptr)) return -6;
   if (!paged && S_fixed < 1) return -7;
@@ -720,9 +957,11 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   p.qrows = H * q_len;
   p.score_c = (float)((double)scale * (double)kv_scale * 1.4426950408889634);
   p.kv_scale = kv_scale;
-  // Request slots per XCD for the snake deal of ranks 0..B-1 (see the kernel).
-  const int slots_per_xcd = 2 * ((B - 1) / 16) + (((B - 1) % 16) >= 8 ? 2 : 1);
-  const long long grid = (long long)mm::kNumXcds * slots_per_xcd * p.parts * p.ngroups;
+  // Unit slots per XCD for the snake deal of units 0..U-1, U <= B * parts (the
+  // kernel's split plan never exceeds that bound; CTAs past the real count exit).
+  const long long umax = (long long)B * p.parts;
+  const long long slots_per_xcd = 2 * ((umax - 1) / 16) + (((umax - 1) % 16) >= 8 ? 2 : 1);
+  const long long grid = (long long)mm::kNumXcds * slots_per_xcd * p.ngroups;
   if (grid > 0x7FFFFFFFLL) return -8;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (paged)
@@ -741,12 +980,14 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
 
 extern "C" {
 
-size_t mla_decode_a16w8_workspace_bytes(void) { return kMaxRecords * (kLat + 2) * sizeof(float); }
+// Records (O [512] + (m, l) per query row and part) plus an 8-byte
+// (parts, first record) entry per request.
+size_t mla_decode_a16w8_workspace_bytes(void) { return kMaxRecords * (kLat + 2) * sizeof(float) + kMaxRecords * 8; }
 
 size_t mla_decode_a16w8_multiq_workspace_for(int B, int H, int parts, int q_len) {
   if (B < 1 || H < 1 || q_len < 1) return 0;
   const int p = clamp_parts(parts, B, H, q_len, true);
-  return (size_t)B * p * H * q_len * (kLat + 2) * sizeof(float);
+  return (size_t)B * p * H * q_len * (kLat + 2) * sizeof(float) + (size_t)B * 8;
 }
 
 int launch_mla_decode_a16w8(const void* q_lat, const void* q_pe, const void* c_kv, const void* k_pe, void* o_lat,

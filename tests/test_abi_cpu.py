@@ -89,7 +89,7 @@ def test_mla_planners():
         assert 1 <= p <= max(1, -(-S // 32))
         eff = _lib.lib.moonmath_mla_effective_parts(B, H, p, ql, 1)
         assert eff == p  # planned parts always fit the workspace
-        assert _lib.lib.mla_decode_a16w8_multiq_workspace_for(B, H, p, ql) == B * p * H * ql * 514 * 4
+        assert _lib.lib.mla_decode_a16w8_multiq_workspace_for(B, H, p, ql) == B * p * H * ql * 514 * 4 + 8 * B
     assert _lib.lib.moonmath_mla_effective_parts(4, 16, 9, 1, 0) == 1  # no workspace -> no split
 
 
@@ -174,3 +174,22 @@ def test_mla_checks_without_device():
         _check_q(q.float(), _bf16(2, 16, 64), _bf16(2, 16, 512), "x", multiq=False)
     with pytest.raises(ValueError, match="same rank"):
         _check_q(q, _bf16(2, 1, 16, 64), _bf16(2, 16, 512), "x", multiq=False)
+
+
+def test_mla_split_plan_fits_workspace():
+    """The device split plan (chunk C = max(512, roundup32(ceil(sumL / (B (P-1))))),
+    ceil(L_b / C) parts per request) never needs more than B * P records, for
+    random and adversarial length mixes; mirrors csrc/mla_decode.hip chunk_tokens."""
+    import numpy as np
+
+    rng = np.random.default_rng(3)
+    cases = [rng.integers(0, 9000, size=int(rng.integers(1, 200))).tolist() for _ in range(300)]
+    cases += [[0] * 7, [1] * 64, [100000] + [1] * 63, [512] * 10, [513] * 10]
+    for lens in cases:
+        B = len(lens)
+        for P in (2, 3, 4, 8, 16):
+            sumL = sum(lens)
+            c = -(-sumL // (B * (P - 1)))
+            c = max(512, -(-c // 32) * 32)
+            total = sum(1 if L <= c else -(-L // c) for L in lens)
+            assert total <= B * P, (lens, P, total)

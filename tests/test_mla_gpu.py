@@ -150,6 +150,27 @@ def test_split_parts_agree(parts):
     _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_192, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
 
 
+@pytest.mark.parametrize("q_len,parts", [(1, 1), (1, 2), (1, 4), (3, 3)])
+def test_paged_large_ragged_batch_balanced_split(q_len, parts):
+    """80 requests (more than one 64-lane chunk of the device-side split plan),
+    lengths from 1 token to 1500 including tile-edge values; the plan cuts long
+    requests into equal parts and dispatches them longest first."""
+    B, H = 80, 8
+    lens = [1, 5, 31, 32, 33, 63, 64, 65, 600, 1500] + ragged_lens(B - 10, 1, 1200, 61)
+    pool, idx, indptr = paged_pool(lens, 61)
+    q_lat, q_pe = rand_q(B, q_len, H, 61)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    if q_len == 1:
+        ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool),
+                                      o[:, 0], _d(lens_t), None, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    else:
+        ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(lens_t), None, _d(idx),
+                                             _d(indptr), parts, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
 def test_paged_rows_remaps_query_and_output():
     """Reference tests/test_mla_decode.py:164-188: reversing rows reverses the batch."""
     B, H, q_len = 4, 16, 4
