@@ -406,30 +406,37 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     stage_idx(kv_lo, seg_end(kv_lo), 0, nm < 64 ? nm : 64);
   }
   bool idx_prestaged = true;
+  // The Q loads are issued right after the first tile's gather (first segment
+  // of the first sweep), so their latency overlaps the tile's.
   bf16x8 qf[2 * kQRegPairs];
+  bool q_ready = false;
+  auto load_q = [&]() {
 #pragma unroll
-  for (int s = 0; s < kQRegPairs; ++s) {
-    const uint16_t* src = p.q_lat + qoff * kLat + s * 32 + g * 16;
-    qf[2 * s] = *reinterpret_cast<const bf16x8*>(src);
-    qf[2 * s + 1] = *reinterpret_cast<const bf16x8*>(src + 8);
-  }
-  // Q dims [448, 576): 32 rows x 16 chunks of 8 bf16 (chunks 0..7 from q_lat,
-  // 8..15 = the rope part from q_pe) into LDS.
+    for (int s = 0; s < kQRegPairs; ++s) {
+      const uint16_t* src = p.q_lat + qoff * kLat + s * 32 + g * 16;
+      qf[2 * s] = *reinterpret_cast<const bf16x8*>(src);
+      qf[2 * s + 1] = *reinterpret_cast<const bf16x8*>(src + 8);
+    }
+    // Q dims [448, 576): 32 rows x 16 chunks of 8 bf16 (chunks 0..7 from q_lat,
+    // 8..15 = the rope part from q_pe) into LDS.
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int id = tid + it * kThreads;  // 512 chunks
-    const int r = id >> 4, c = id & 15;
-    const int rr = grp * kRowsPerCta + r;
-    const long long ro = (long long)qb * p.qrows + (rr < p.qrows ? rr : p.qrows - 1);
-    const uint16_t* src = (c < 8) ? p.q_lat + ro * kLat + kQLdsDim0 + c * 8 : p.q_pe + ro * kRope + (c - 8) * 8;
-    *reinterpret_cast<bf16x8*>(qpe_lds + r * kQLdsRowBytes + 16 * (c ^ (r & 15))) = *reinterpret_cast<const bf16x8*>(src);
-  }
-
-  // Retire the Q and index loads here, visibly to the compiler (vmcnt 0,
-  // expcnt/lgkmcnt untouched): the tile DMAs are invisible to its wait-count
-  // model, so a wait left to the loop would become a per-tile vmcnt countdown
-  // that also waits for the prefetched tile.
-  __builtin_amdgcn_s_waitcnt(0x0F70);
+    for (int it = 0; it < 2; ++it) {
+      const int id = tid + it * kThreads;  // 512 chunks
+      const int r = id >> 4, c = id & 15;
+      const int rr = grp * kRowsPerCta + r;
+      const long long ro = (long long)qb * p.qrows + (rr < p.qrows ? rr : p.qrows - 1);
+      const uint16_t* src = (c < 8) ? p.q_lat + ro * kLat + kQLdsDim0 + c * 8 : p.q_pe + ro * kRope + (c - 8) * 8;
+      *reinterpret_cast<bf16x8*>(qpe_lds + r * kQLdsRowBytes + 16 * (c ^ (r & 15))) =
+          *reinterpret_cast<const bf16x8*>(src);
+    }
+    // Retire every load here, visibly to the compiler (vmcnt 0, expcnt/lgkmcnt
+    // untouched; this also lands the first tile): the tile DMAs are invisible
+    // to its wait-count model, so a wait left to the loop would become a
+    // per-tile vmcnt countdown that also waits for the prefetched tile.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // qpe_lds published
+    q_ready = true;
+  };
 
   // ---- per-lane constant offsets inside a staged tile -------------------------------
   // K read of pair s: token n, piece 2s+g -> n*576 + 16*((2s+g) ^ swz(n)).
@@ -486,10 +493,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
         const int nb = (nmine - i0 < 64) ? nmine - i0 : 64;
         if (!(idx_prestaged && seg_lo == kv_lo && i0 == 0)) stage_idx(seg_lo, seg_hi, i0, nb);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll 4
         for (int q = 0; q < (nb + 1) / 2; ++q) {
           const int i = i0 + 2 * q + g;
           const int v = *reinterpret_cast<const int*>(wring + kIdxStageInRing + 256 * q + 4 * lane);
-          const int first = __shfl(v, 32 * g);
+          const int f0 = __builtin_amdgcn_readlane(v, 0), f1 = __builtin_amdgcn_readlane(v, 32);
+          const int first = g ? f1 : f0;
           const int tok = seg_lo + kTileTok * (wave + kWaves * i) + n;
           const unsigned long long bal = __builtin_amdgcn_ballot_w64(tok >= seg_hi || v == first + n);
           const bool contiguous = ((bal >> (32 * g)) & 0xffffffffull) == 0xffffffffull;
@@ -498,7 +507,6 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
       }
     }
     idx_prestaged = false;  // a later sweep re-stages its indices
-    if (seg_lo == kv_lo) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");  // qpe_lds
     const int eff = lim < seg_hi ? lim : seg_hi;  // this row's token limit in the segment
 
     // Gather of tile j (tokens seg_lo + 32j ..), j = wave + 4i. Fast path: the
@@ -555,6 +563,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
 
     int slot = 0;
     if (wave < ntiles) issue_tile(wave, wring);
+    if (!q_ready) load_q();  // CTA-uniform: the first segment of the first sweep
     for (int j = wave; j < ntiles; j += kWaves) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile has landed
       const char* st = wring + slot * kTileBytes;
@@ -754,8 +763,12 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   L = xor32_sum(L);  // whole-row sum (lanes n and n+32)
   const bool split = un.nparts > 1;
   const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
-  const size_t rec = ((size_t)un.rec0 + part) * p.qrows + qrow;
-  uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow) * kLat;
+  // The query row again, from the lane id (cheaper than keeping it live
+  // through the tile loop).
+  const int qrow_e = grp * kRowsPerCta + (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
+  const bool row_ok_e = qrow_e < p.qrows;
+  const size_t rec = ((size_t)un.rec0 + part) * p.qrows + qrow_e;
+  uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow_e) * kLat;
   float* prow = p.ws + rec * kLat;
 
 #pragma unroll
@@ -790,7 +803,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
         }
         // Lane (n, g), register 4*i4 + e of d-tile dt: dim 32dt + 8*i4 + 4g + e.
         const int d = 32 * dt + 8 * i4 + 4 * g;
-        if (row_ok) {
+        if (row_ok_e) {
           if (split) {
             *reinterpret_cast<f32x4*>(prow + d) = acc;
           } else {
@@ -803,7 +816,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
       }
     }
   }
-  if (split && row_ok && g == 0 && wave == 0) {
+  if (split && row_ok_e && g == 0 && wave == 0) {
     float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + rec * 2;
     pml[0] = M;
     pml[1] = L;
