@@ -46,7 +46,7 @@ constexpr int kFragBytes = 1024;   // one 32x16 bf16 MFMA operand fragment (64 l
 constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
 constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
 constexpr int kVtBlockElems = kKvBlock * kD; // 8192 bf16 per V_t block
-constexpr int kLdsBytes = 2 * (kKBytes + kVBytes) + 64;  // 2-slot K and V_t rings + votes
+constexpr int kLdsBytes = 2 * (kKBytes + kVBytes) + 64;  // 2-slot K and V_t rings + votes [2][kWaves]
 // Pass 0 accepts blocks whose per-lane sum of p stays <= 2^kGrowLog2, which
 // bounds every p by that value (no fp32 overflow of O for |v| < 2^90).
 constexpr float kGrowLimit = 1048576.0f;     // 2^20
@@ -245,7 +245,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
-    if (tid < kWaves) votes[tid] = 0;
+    if (tid < 2 * kWaves) votes[tid] = 0;
     issue_k(kb_begin, 0);
     if (kb_begin + 1 < kb_end) issue_k(kb_begin + 1, 1);
     issue_v(kb_begin, 0);
@@ -261,14 +261,18 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       sched_fence();
       lds_reads_done_barrier_vm0();
       sched_fence();
-      const int vote_any = votes[0] | votes[1] | votes[2] | votes[3];
+      // Votes are double-buffered by step parity: step i reads exactly step
+      // i - 1's votes (written before this barrier), never a faster wave's
+      // vote of step i, so every wave takes the same abort decision.
+      const int* vp = votes + ((i + 1) & 1) * kWaves;
+      const int vote_any = vp[0] | vp[1] | vp[2] | vp[3];
       if (kb + 2 < kb_end) issue_k(kb + 2, i & 1);
       if (kb + 1 < kb_end) issue_v(kb + 1, (i + 1) & 1);
       mask(scur, kb);
       qk(kring + ((i + 1) & 1) * kKBytes, snext);  // last block: stale slot, unused
       const float lblk = softmax(scur, pf);
       row_l += lblk;
-      votes[wave] = __builtin_amdgcn_ballot_w64(!(lblk <= kGrowLimit) && lblk == lblk) != 0;
+      votes[(i & 1) * kWaves + wave] = __builtin_amdgcn_ballot_w64(!(lblk <= kGrowLimit) && lblk == lblk) != 0;
       pv(vring + (i & 1) * kVBytes, pf);
       return vote_any != 0;
     };
@@ -278,7 +282,10 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     }
     sched_fence();
     lds_reads_done_barrier_vm0();
-    if (!aborted) aborted = (votes[0] | votes[1] | votes[2] | votes[3]) != 0;
+    if (!aborted) {
+      const int* vp = votes + ((nblk - 1) & 1) * kWaves;  // the last step's votes
+      aborted = (vp[0] | vp[1] | vp[2] | vp[3]) != 0;
+    }
   }
   if (aborted) {
     // Fallback for rows whose max grew past kGrowLimit: walk the range again

@@ -134,19 +134,6 @@ __device__ __forceinline__ void pv_mfma(f32x16& acc, bf16x8 a, bf16x8 b) {
   asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-// 16-byte global -> LDS DMA issued through asm. The kernel counts these loads
-// itself (explicit s_waitcnt vmcnt); hiding them from the compiler keeps it
-// from adding a conservative vmcnt(0) before every LDS transpose read (it
-// cannot prove those reads do not alias an in-flight DMA).
-__device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_dst) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
-}
-// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane offset.
-__device__ __forceinline__ void dma16_sbase(const void* sbase, uint32_t voff, const char* lds_dst) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
-}
 // Field `k` (16 bits) of a packed pair, extracted where it is used (volatile:
 // not hoisted, so the packed pairs are what stays live).
 __device__ __forceinline__ uint32_t u16_field(uint32_t w, int k) {

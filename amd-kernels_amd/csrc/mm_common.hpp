@@ -133,6 +133,20 @@ __device__ __forceinline__ void dma16(const void* gsrc, MM_LDS void* lds_dst) {
   __builtin_amdgcn_global_load_lds(gsrc, lds_dst, 16, 0, 0);
 }
 
+// The same DMA issued through asm, for kernels that count their loads
+// themselves (explicit s_waitcnt vmcnt): hidden from the compiler's wait-count
+// model, it cannot trigger a conservative vmcnt(0) before LDS reads that the
+// compiler cannot prove disjoint from an in-flight DMA. lds_dst is a generic
+// pointer into __shared__ memory, wave-uniform.
+__device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
+}
+// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane offset.
+__device__ __forceinline__ void dma16_sbase(const void* sbase, uint32_t voff, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
+}
 // Barrier without the implicit vmcnt(0) that __syncthreads() carries, so
 // prefetch DMA stays in flight across it. VMEM_LEFT = loads allowed to remain
 // outstanding (issued after the data the barrier publishes).
