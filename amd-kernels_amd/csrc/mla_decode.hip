@@ -47,41 +47,22 @@
 
 #include <type_traits>
 
-#include "mm_common.hpp"
+#include "mla_common.hpp"
 
 namespace mm {
 namespace mla {
 
-constexpr int kLat = 512;
-constexpr int kRope = 64;
-constexpr int kQK = kLat + kRope;              // 576 bytes per fp8 row
-constexpr int kTileTok = 32;                   // tokens per tile
-constexpr int kTileBytes = kTileTok * kQK;     // 18432 fp8 bytes per tile
-constexpr int kDmaPerTile = kTileBytes / 1024; // 18 wave-DMA instructions (64 x 16 B)
 constexpr int kRowsPerCta = 32;                // query rows per CTA (one MFMA tile)
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKPairs = kQK / 32;              // 18 pairs of 16-dim k-steps (16 latent + 2 rope)
-constexpr int kDTiles = kLat / 32;             // 16 output d-tiles of 32
-constexpr int kMaxQLen = 8;
-constexpr int kMaxHeads = 128;
 constexpr int kTabPerWave = 512;               // tile-table entries per wave (one segment)
-// A row's running max is fixed at its first non-empty tile; later tiles may
-// exceed it by up to 2^64 (p <= 2^64, no fp32 overflow of O or l). Beyond that
-// the CTA falls back to an exact-max second pass.
-constexpr float kGrowLimit = 64.f;
 
 // LDS map (bytes): per-wave 2-slot tile rings, per-wave tile tables (base slot
-// of each of the wave's tiles in the current segment), the rope part of Q. The
-// merge at the end reuses the tile rings.
+// of each of the wave's tiles in the current segment), the LDS-resident Q
+// dims of the CTA's 32 rows. The merge at the end reuses the tile rings.
 constexpr int kRingBytes = 2 * kTileBytes;                  // 36864 per wave
 constexpr int kStageBytes = kWaves * kRingBytes;            // 147456
 constexpr int kTabOff = kStageBytes;
-// Q dims [448, 576) (the last four k-step pairs) of the CTA's 32 rows stay in
-// LDS: 256 B per row, 16-byte chunk c of row r at chunk c ^ (r & 15).
-constexpr int kQRegPairs = 14;                 // k-step pairs whose Q lives in VGPRs
-constexpr int kQLdsDim0 = kQRegPairs * 32;     // 448
-constexpr int kQLdsRowBytes = (kQK - kQLdsDim0) * 2;  // 256
 constexpr int kQpeOff = kTabOff + kWaves * kTabPerWave * 4;  // 155648
 constexpr int kLdsBytes = kQpeOff + kRowsPerCta * kQLdsRowBytes;  // 163840
 // Staged slot indices: the last 8 KB of each wave's own ring (2048 indices).
@@ -91,221 +72,8 @@ constexpr int kMergeOBytes = 8 * 4 * 64 * 16;              // 32768 per wave and
 static_assert(kWaves * kMergeOBytes <= kStageBytes, "merge area fits the rings");
 static_assert(2 * 64 + 1 <= kTabPerWave, "(m, l) and the fallback flag fit a wave's tile table");
 
-// Split partial records: one per (b, part, query row): O [512] fp32, then all
-// (m, l) pairs after the last O record. kMaxRecords caps the workspace.
-constexpr size_t kMaxRecords = 65536;
-
-struct Params {
-  const uint16_t* q_lat;  // [B, q_len, H, 512] bf16 (q_len 1: [B, H, 512])
-  const uint16_t* q_pe;   // [B, q_len, H, 64]
-  const uint8_t* kv;      // paged: [slots, 576] fp8; contiguous: [B, S, 576]
-  uint16_t* o_lat;        // like q_lat
-  float* ws;              // split partials (parts > 1)
-  const int* seq_lens;    // [B] (paged)
-  const int* rows;        // [B] q/out row per request, or null
-  const int* kv_indices;  // flat per-token slots (paged)
-  const int* kv_indptr;   // [B+1] (paged)
-  int B, H, q_len, S_fixed, parts, ngroups, paged;
-  int qrows;              // H * q_len
-  float score_c;          // scale * kv_scale * log2(e), fp32
-  float kv_scale;
-};
-
-typedef int i32x2 __attribute__((ext_vector_type(2)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-// Two fp8 of a dword (lo or hi half) -> two bf16, exact (scale 1).
-template <bool HI>
-__device__ __forceinline__ uint32_t fp8x2_bf16(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
-}
-__device__ __forceinline__ bf16x8 fp8x8_bf16(uint32_t lo, uint32_t hi) {
-  u32x4 o = {fp8x2_bf16<false>(lo), fp8x2_bf16<true>(lo), fp8x2_bf16<false>(hi), fp8x2_bf16<true>(hi)};
-  return __builtin_bit_cast(bf16x8, o);
-}
-
-// O^T += V^T P^T into an AGPR accumulator. The s_nop covers the VALU-write ->
-// MFMA-read distance for operands converted just before (the compiler cannot
-// see through the asm); consecutive calls always target different
-// accumulators, and every VALU read of an accumulator is preceded by
-// mfma_result_fence().
-__device__ __forceinline__ void pv_mfma(f32x16& acc, bf16x8 a, bf16x8 b) {
-  asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-
-// Field `k` (16 bits) of a packed pair, extracted where it is used (volatile:
-// not hoisted, so the packed pairs are what stays live).
-__device__ __forceinline__ uint32_t u16_field(uint32_t w, int k) {
-  uint32_t r;
-  asm volatile("v_bfe_u32 %0, %1, %2, 16" : "=v"(r) : "v"(w), "i"(16 * k));
-  return r;
-}
-
-// ---- split plan ------------------------------------------------------------------------
-// The caller's `parts` P is a budget: with sumL the total context of the batch,
-// every request is cut into chunks of C tokens,
-//   C = max(512, roundup32(ceil(sumL / (B (P - 1)))))   (P > 1),
-// request b getting nparts_b = ceil(L_b / C) parts (at least 1). Because
-// ceil(L/C) < L/C + 1, sum_b nparts_b < sumL / C + B <= B P: the partial records
-// always fit the B * P * qrows workspace. Parts of one request have equal token
-// counts except the last, so CTAs carry similar work whatever the lengths.
-constexpr int kMinChunk = 512;
-// The paged plan keeps three B-entry tables in one wave's tile ring.
-constexpr int kMaxPagedB = kRingBytes / 12;  // 3072
-
-__device__ __forceinline__ int chunk_tokens(long long sumL, int B, int P) {
-  if (P <= 1) return 0x7FFFFFE0;
-  long long c = (sumL + (long long)B * (P - 1) - 1) / ((long long)B * (P - 1));
-  c = (c + kTileTok - 1) / kTileTok * kTileTok;
-  if (c < kMinChunk) c = kMinChunk;
-  return c > 0x7FFFFFE0 ? 0x7FFFFFE0 : (int)c;
-}
-__device__ __forceinline__ int nparts_of(int L, int C) { return L <= C ? 1 : (L + C - 1) / C; }
-// Tokens per part of a request of L tokens in np parts: equal shares rounded up
-// to whole tiles (the last part takes the remainder).
-__device__ __forceinline__ int part_tokens(int L, int np) {
-  const int t = (L + np - 1) / np;
-  return (t + kTileTok - 1) / kTileTok * kTileTok;
-}
-
-// Wave64 reductions and inclusive scan on DPP row shifts / broadcasts (no LDS).
-__device__ __forceinline__ int wave_incl_scan(int v);
-__device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
-__device__ __forceinline__ int wave_max_i(int v) {
-  // Invalid DPP sources return `old` = the lane's own value (neutral for max).
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));
-  return __builtin_amdgcn_readlane(v, 63);
-}
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
-  return v;
-}
-
-struct Unit {
-  int b;       // request
-  int part;    // part within the request
-  int nparts;  // parts of the request
-  int rec0;    // record part index of the request's part 0 (request-index order)
-  int ptok;    // tokens per part of this request
-  int units;   // total units (request parts) in the batch
-};
-
-// Unit `u` of the batch in longest-first order: requests sorted into 16 linear
-// buckets of their part size (largest first, request index inside a bucket),
-// each request's parts consecutive. Wave-uniform; every wave of a CTA computes
-// it on its own, using `scratch` (12 * B bytes of this wave's LDS).
-__device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int lane, int* scratch) {
-  int* lens = scratch;            // [B] lengths, then part sizes
-  int* req_at = scratch + B;      // [B] request at each position
-  int* np_at = scratch + 2 * B;   // [B] parts of the request at each position
-  long long suml = 0;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const int l = (c0 + lane < B) ? seq_lens[c0 + lane] : 0;
-    if (c0 + lane < B) lens[c0 + lane] = l;
-    suml += wave_sum_i(l);  // per-chunk sums stay below 2^31 for lengths < 2^25
-  }
-  const int C = chunk_tokens(suml, B, P);
-  int maxp = 0;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const bool valid = c0 + lane < B;
-    const int l = valid ? lens[c0 + lane] : 0;
-    const int pt = valid ? part_tokens(l, nparts_of(l, C)) : 0;
-    maxp = max(maxp, wave_max_i(pt));
-  }
-  maxp = __builtin_amdgcn_readfirstlane(maxp);
-  auto bucket_of = [&](int pt) {  // 0 = largest parts
-    const long long q = (long long)pt * 16 / ((long long)maxp + 1);
-    return 15 - (int)q;
-  };
-  int start[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) start[k] = 0;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const bool valid = c0 + lane < B;
-    const int l = valid ? lens[c0 + lane] : 0;
-    const int bk = valid ? bucket_of(part_tokens(l, nparts_of(l, C))) : -1;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) start[k] += __builtin_popcountll(__builtin_amdgcn_ballot_w64(bk == k));
-  }
-  int acc = 0;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int c = start[k];
-    start[k] = acc;
-    acc += c;
-  }
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const bool valid = c0 + lane < B;
-    const int l = valid ? lens[c0 + lane] : 0;
-    const int np = nparts_of(l, C);
-    const int bk = valid ? bucket_of(part_tokens(l, np)) : -1;
-    int pos = 0;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const unsigned long long m = __builtin_amdgcn_ballot_w64(bk == k);
-      if (bk == k) pos = start[k] + __builtin_popcountll(m & lt);
-      start[k] += __builtin_popcountll(m);
-    }
-    if (valid) {
-      req_at[pos] = c0 + lane;
-      np_at[pos] = np;
-    }
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  Unit r{0, 0, 1, 0, kTileTok, 0};
-  int run = 0;  // units before this chunk of positions
-  bool found = false;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const bool valid = c0 + lane < B;
-    const int np = valid ? np_at[c0 + lane] : 0;
-    const int inc = wave_incl_scan(np);
-    const int excl = run + inc - np;
-    const unsigned long long hit = __builtin_amdgcn_ballot_w64(valid && u >= excl && u < excl + np);
-    if (!found && hit) {
-      const int hl = (int)__builtin_ctzll(hit);
-      r.b = __builtin_amdgcn_readlane(req_at[c0 + lane], hl);
-      r.part = u - __builtin_amdgcn_readlane(excl, hl);
-      r.nparts = __builtin_amdgcn_readlane(np, hl);
-      found = true;
-    }
-    run += __builtin_amdgcn_readlane(inc, 63);
-  }
-  r.units = run;
-  r.ptok = part_tokens(lens[r.b], r.nparts);
-  // Record offset: parts of the requests before b, in request-index order.
-  int rec0 = 0;
-  for (int c0 = 0; c0 < B; c0 += 64) {
-    const int idx = c0 + lane;
-    rec0 += wave_sum_i(idx < B && idx < r.b ? nparts_of(lens[idx], C) : 0);
-  }
-  r.rec0 = rec0;
-  return r;
-}
-
-// 4-byte global -> LDS DMA (lane l's dword lands at lds_dst + 4*l), counted by
-// the kernel itself like dma16_opaque.
-__device__ __forceinline__ void dma4_opaque(const void* gsrc, const char* lds_dst) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
-  asm volatile("global_load_lds_dword %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
-}
-
-// Staging layout of one tile: token t's 576-byte row at t*576, its 16-byte
-// piece c stored at piece slot c ^ swz(t) (a permutation inside each aligned
-// group of 4 pieces) so the 32 lanes of a K read and the 8-token groups of a
-// V^T transpose read hit distinct LDS banks.
-__device__ __forceinline__ int swz(int t) { return (t >> 2) & 3; }
+// The paged plan's 12 * B bytes of scratch live in one wave's tile ring.
+static_assert(12 * kMaxPagedB <= kRingBytes, "plan scratch fits a wave's ring");
 
 template <bool PAGED>
 __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
@@ -889,7 +657,18 @@ constexpr int kQRowsPerCta = kRowsPerCta;  // 32
 constexpr int kNumCUs = 256;
 constexpr int kMaxParts = 64;
 
-int ngroups_for(int H, int q_len) { return (H * q_len + kQRowsPerCta - 1) / kQRowsPerCta; }
+// Requests of 96..128 query rows (H * q_len) run mla_wide_kernel (one 128-row
+// block per CTA); others the 32-row kernel. Measured at B=64, ctx U[1024,8192]
+// (steady clocks): H=128 q_len 1: 118 us wide vs 132 us 32-row; H=128 q_len 2
+// (two row blocks): 213 us wide vs 185 us 32-row -- with several row blocks the
+// split records (rows x parts x 2 KB) outweigh the shared tile loads.
+constexpr int kWideMinRows = 96;
+constexpr int kWideRowsPerCta = 128;
+bool use_wide(int H, int q_len) { return H * q_len >= kWideMinRows && H * q_len <= kWideRowsPerCta; }
+int ngroups_for(int H, int q_len) {
+  const int rows = use_wide(H, q_len) ? kWideRowsPerCta : kQRowsPerCta;
+  return (H * q_len + rows - 1) / rows;
+}
 
 // Largest parts the fixed record workspace allows for (B, H, q_len).
 int max_parts_for(int B, int H, int q_len) {
@@ -900,16 +679,17 @@ int max_parts_for(int B, int H, int q_len) {
 }
 
 // Split planner. The kernel cuts requests into equal chunks so that the batch
-// has about B * (parts - 1) + B/2 units (request parts); aim at ~1.5 rounds of
-// CTAs over the CUs for wide query rows (4+ row groups) and one round for
-// narrow ones (per-CTA set-up dominates short CTAs), within the record cap.
+// has about B * (parts - 1) + B/2 units (request parts), within the record
+// cap. 32-row kernel: one round of CTAs over the CUs (one CTA per CU fits in
+// LDS; per-CTA set-up dominates short CTAs). 128-row kernel: about one unit per
+// CU whatever the number of row blocks (measured: B=64, H=128, q_len 2 runs
+// 209 us with 4 parts and 448 CTAs, 264 us with 2 parts and 192 CTAs).
 int plan_parts(int B, int H, int max_seq_len, int q_len) {
   if (B < 1) B = 1;
   if (q_len < 1) q_len = 1;
   const int ng = ngroups_for(H, q_len);
   // Units ~ B * (p - 1) + B / 2 (see the kernel's chunking).
-  const int ctas = ng >= 4 ? (3 * kNumCUs) / 2 : kNumCUs;
-  const int units = ctas / ng;
+  const int units = use_wide(H, q_len) ? kNumCUs : kNumCUs / ng;
   int p = units > B / 2 ? 1 + (units - B / 2) / B : 1;
   const int by_len = 1 + max_seq_len / 512;  // chunks are at least 512 tokens
   if (p > by_len) p = by_len;
@@ -964,7 +744,9 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   const long long grid = (long long)mm::kNumXcds * slots_per_xcd * p.ngroups;
   if (grid > 0x7FFFFFFFLL) return -8;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (paged)
+  if (use_wide(H, q_len))
+    launch_wide_kernel(p, grid, st);
+  else if (paged)
     hipLaunchKernelGGL(mla_decode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);

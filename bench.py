@@ -35,15 +35,31 @@ def attention_flops(B, H, Sq, Skv, D=128):
     return 4.0 * B * H * Sq * Skv * D
 
 
+# Seconds of back-to-back work before each timed region, so clocks have settled
+# (measured on MI355X: after only a few ms of warmup the MLA decode timed 10-15%
+# slower than in steady state).
+WARM_S = 0.25
+
+
+def _warm(torch, fn, calls):
+    """Run fn(i) at least `calls` times and until WARM_S seconds have passed."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < calls or time.perf_counter() - t0 < WARM_S:
+        fn(i)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def bench_attention(args, torch, ma, _lib):
     B, S, H = 2, 8192, 24
     mode = args.mode
     g = torch.Generator().manual_seed(42)
     q, k, v = (torch.randn(B, S, H, 128, generator=g).to(torch.bfloat16).to("cuda:0") for _ in range(3))
     out = torch.empty_like(q)
-    for _ in range(args.warmup):
-        ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd")
-    torch.cuda.synchronize()
+    _warm(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.warmup)
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -129,9 +145,7 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
                 ma.mla_decode_a16w8_paged_dev(q_lat[:, 0], q_pe[:, 0], pool, o[:, 0], lens_t, None, idx, indptr,
                                               parts, SCALE_192, KV_SCALE)
 
-        for r in range(warmup):
-            call(r)
-        torch.cuda.synchronize()
+        _warm(torch, call, warmup)
         st = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(st)

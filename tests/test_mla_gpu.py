@@ -171,6 +171,56 @@ def test_paged_large_ragged_batch_balanced_split(q_len, parts):
     _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
 
 
+@pytest.mark.parametrize("H,q_len,parts", [(128, 1, 1), (128, 1, 3), (100, 1, 2), (64, 3, 2), (16, 8, 1)])
+def test_wide_block_ragged_tile_edges(H, q_len, parts):
+    """Query blocks of >= 96 rows run the 128-row kernel: lengths at tile edges
+    (1, 31..33, 63..65 tokens), partial row tiles (H=100, 3 x 64 rows) and split
+    parts, paged over a permuted pool."""
+    lens = [1, 5, 31, 32, 33, 63, 64, 65, 97, 600, 1500, 2100]
+    B = len(lens)
+    pool, idx, indptr = paged_pool(lens, 67)
+    q_lat, q_pe = rand_q(B, q_len, H, 67)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    if q_len == 1:
+        ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool),
+                                      o[:, 0], _d(lens_t), None, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    else:
+        ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(lens_t), None, _d(idx),
+                                             _d(indptr), parts, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+@pytest.mark.parametrize("H", [16, 128])
+def test_max_fallback_on_growing_scores(H):
+    """Scores that rise more than 2^64 above a row's first tile send the CTA
+    through the exact-max fallback (a max-only pass, then accumulation with
+    the row max fixed); the result must still match the exact-max oracle."""
+    # Only q dims 0..100 are non-zero. Tokens >= lo carry k = 448 in dims 0..99
+    # and a random k in dim 100 with |k| >= 1/16, so their scores (up to 9e4,
+    # times c: ~170 on the log2 grid, vs ~0 for the first tokens) are sums of
+    # products on a 2^-7 grid below 2^17: exact in fp32 in any order. (Random
+    # scores of that size would carry fp32 accumulation-order noise of ~1e-5 in
+    # the exponent, which flips bf16(P) far more often than the exactness bar
+    # allows, in any correct kernel.)
+    B, S, lo = 2, 300, 40
+    g = torch.Generator().manual_seed(71)
+    kv = rand_kv_rows(B * S, 71).view(B, S, QK)
+    kv[:, lo:, :100] = torch.full((B, S - lo, 100), 448.0).to(torch.float8_e4m3fn)
+    k100 = kv[:, lo:, 100].float()
+    kv[:, lo:, 100] = torch.where(k100.abs() < 0.0625, torch.full_like(k100, 0.0625), k100).to(torch.float8_e4m3fn)
+    q_lat = torch.zeros(B, H, 512)
+    q_lat[..., :100] = torch.randint(1, 3, (B, H, 100), generator=g).float()  # 1 or 2
+    q_lat[..., 100] = 2.0 ** torch.randint(-1, 2, (B, H), generator=g).float()  # 0.5, 1 or 2
+    q_lat = q_lat.to(torch.bfloat16)
+    q_pe = torch.zeros(B, H, 64, dtype=torch.bfloat16)
+    o = torch.zeros(B, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8(_d(q_lat), _d(q_pe), _d(kv), o, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(kv), [S] * B, SCALE_576)
+
+
 def test_paged_rows_remaps_query_and_output():
     """Reference tests/test_mla_decode.py:164-188: reversing rows reverses the batch."""
     B, H, q_len = 4, 16, 4
