@@ -11,7 +11,8 @@
 //    column and 16 kv rows per 32x32 tile; P^T then feeds O^T = V^T P^T as the
 //    B operand straight from registers (no shuffle).
 //  * K and the pre-transposed V_t are staged through LDS with 16-byte
-//    global->LDS DMA (global_load_lds_dwordx4), double buffered. K is stored
+//    global->LDS DMA (global_load_lds_dwordx4) in 4-slot rings, two blocks of
+//    lead. K is stored
 //    in MFMA fragment order so every operand read is a conflict-free
 //    ds_read_b128 at base + 16*lane.
 //  * Online softmax in base 2 with the running max kept on the integer grid:
@@ -38,7 +39,7 @@ namespace attn {
 
 constexpr int kD = 128;            // head_dim
 constexpr int kKvBlock = 64;       // kv rows per main-loop block
-constexpr int kWaves = 4;          // waves per CTA (one per SIMD; two CTAs per CU)
+constexpr int kWaves = 8;          // waves per CTA (two per SIMD; one CTA per CU)
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQRowsPerTile = 32;  // q rows per wave = one 32x32 MFMA tile
 constexpr int kRowsPerCta = kWaves * kQRowsPerTile;  // 128
@@ -46,7 +47,8 @@ constexpr int kFragBytes = 1024;   // one 32x16 bf16 MFMA operand fragment (64 l
 constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
 constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
 constexpr int kVtBlockElems = kKvBlock * kD; // 8192 bf16 per V_t block
-constexpr int kLdsBytes = 2 * (kKBytes + kVBytes) + 64;  // 2-slot K and V_t rings + votes [2][kWaves]
+constexpr int kRing = 4;           // K / V_t ring slots: block j lives in slot j % kRing
+constexpr int kLdsBytes = kRing * (kKBytes + kVBytes) + 2 * kWaves * 4;  // rings + votes [2][kWaves]
 // Pass 0 accepts blocks whose per-lane sum of p stays <= 2^kGrowLog2, which
 // bounds every p by that value (no fp32 overflow of O for |v| < 2^90).
 constexpr float kGrowLimit = 1048576.0f;     // 2^20
@@ -77,10 +79,14 @@ __device__ __forceinline__ long long head_base(int b, int h, int S, int H, int b
   return bshd ? ((long long)b * S * H + h) * kD : ((long long)b * H + h) * (long long)S * kD;
 }
 
-// One CTA = 4 waves = 128 q rows of one (b, h); two CTAs share a CU. Wave w
-// owns rows [32w, 32w+32). Per 64-row kv block j:
+// One CTA = 8 waves (two per SIMD) = 256 q rows of one (b, h), one CTA per CU,
+// so every K / V_t block is gathered once per CU. Wave w owns rows
+// [32w, 32w+32). Per 64-row kv block j:
 //     QK(j+1) MFMAs || softmax(j) VALU      then      PV(j) MFMAs
-// K and V_t stream through 2-slot LDS rings, DMA'd one block ahead.
+// K and V_t stream through 4-slot LDS rings (128 KB): block j+3 is gathered
+// while block j is processed, so each DMA has two blocks of lead (measured at
+// the headline shape: 1.485 ms vs 1.621 ms for two 128-row CTAs per CU with
+// 2-slot rings and one block of lead).
 //
 // Max policy: the running max m is an integer (log2 units) and is FIXED for the
 // main pass over the kv range, so O and l are never rescaled in the loop:
@@ -114,13 +120,14 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // (coalesced 256-byte reads) and the MFMA fragment reads are conflict free.
   // V_t slot: fragments [t(2)][s(2)][dt(4)], 1 KB each in lane order.
   char* kring = lds;
-  char* vring = lds + 2 * kKBytes;
-  int* votes = reinterpret_cast<int*>(lds + 2 * (kKBytes + kVBytes));
-  // Lane byte offsets of this wave's 4 K-DMA instructions within a block.
-  uint32_t koff[4];
+  char* vring = lds + kRing * kKBytes;
+  int* votes = reinterpret_cast<int*>(lds + kRing * (kKBytes + kVBytes));
+  // Lane byte offsets of this wave's 2 K-DMA instructions within a block (16
+  // instructions of 4 rows each per block, 2 per wave).
+  uint32_t koff[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (wave * 4 + i) * 4 + (lane >> 4);
+  for (int i = 0; i < 2; ++i) {
+    const int row = (wave * 2 + i) * 4 + (lane >> 4);
     koff[i] = (uint32_t)(row * row_stride * 2) + (uint32_t)((((lane & 15) ^ (row & 15))) * 16);
   }
   const long long kblk_bytes = (long long)kKvBlock * row_stride * 2;
@@ -129,25 +136,25 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     if ((kb + 1) * kKvBlock <= p.Skv) {
       const char* base = kh + kb * kblk_bytes;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(base + koff[i], (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
+      for (int i = 0; i < 2; ++i) dma16(base + koff[i], (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
     } else {
       // Last partial block: clamp rows past Skv (they are masked in softmax).
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (wave * 4 + i) * 4 + (lane >> 4);
+      for (int i = 0; i < 2; ++i) {
+        const int row = (wave * 2 + i) * 4 + (lane >> 4);
         int kv = kb * kKvBlock + row;
         kv = kv < p.Skv ? kv : p.Skv - 1;
         dma16(kh + (long long)kv * row_stride * 2 + (((lane & 15) ^ (row & 15)) * 16),
-              (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
+              (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
       }
     }
   };
-  const uint32_t voff = (uint32_t)(wave * 4 * kFragBytes + lane * 16);
+  const uint32_t voff = (uint32_t)(wave * 2 * kFragBytes + lane * 16);
   auto issue_v = [&](int kb, int slot) {
     char* st = vring + slot * kVBytes;
     const char* base = vth + (long long)kb * kVBytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(base + voff + i * kFragBytes, (MM_LDS void*)(st + (wave * 4 + i) * kFragBytes));
+    for (int i = 0; i < 2; ++i) dma16(base + voff + i * kFragBytes, (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
   };
 
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
@@ -246,10 +253,22 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
     if (tid < 2 * kWaves) votes[tid] = 0;
-    issue_k(kb_begin, 0);
-    if (kb_begin + 1 < kb_end) issue_k(kb_begin + 1, 1);
-    issue_v(kb_begin, 0);
-    wait_vmem_barrier<0>();
+    // Blocks 0..2 in flight; block j lives in slot j % kRing.
+    auto issue_kv = [&](int kb, int slot) {
+      issue_k(kb, slot);
+      issue_v(kb, slot);
+    };
+    issue_kv(kb_begin, 0);
+    if (nblk > 1) issue_kv(kb_begin + 1, 1);
+    if (nblk > 2) issue_kv(kb_begin + 2, 2);
+    // 4 DMAs per wave per block: block 0 has landed, blocks 1 and 2 stay in flight.
+    if (nblk > 2) {
+      wait_vmem_barrier<8>();
+    } else if (nblk > 1) {
+      wait_vmem_barrier<4>();
+    } else {
+      wait_vmem_barrier<0>();
+    }
     qk(kring, sA);
     mask(sA, kb_begin);
     row_m = fmaxf(block_max(sA), kNegFltMax);
@@ -257,23 +276,29 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     // One block: returns true when some wave voted to abort (seen one block late).
     auto step = [&](int kb, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
       const int i = kb - kb_begin;
-      // K(kb+1) and V(kb) have landed; every wave is done reading K(kb) and V(kb-1).
+      // Block i+1 has landed (block i+2 stays in flight, 4 DMAs per wave); every
+      // wave is done with step i-1, so the slot of block i-1 is free.
       sched_fence();
-      lds_reads_done_barrier_vm0();
+      if (i + 2 < nblk) {
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
       sched_fence();
       // Votes are double-buffered by step parity: step i reads exactly step
       // i - 1's votes (written before this barrier), never a faster wave's
       // vote of step i, so every wave takes the same abort decision.
       const int* vp = votes + ((i + 1) & 1) * kWaves;
-      const int vote_any = vp[0] | vp[1] | vp[2] | vp[3];
-      if (kb + 2 < kb_end) issue_k(kb + 2, i & 1);
-      if (kb + 1 < kb_end) issue_v(kb + 1, (i + 1) & 1);
+      int vote_any = 0;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) vote_any |= vp[v];
+      if (i + 3 < nblk) issue_kv(kb + 3, (i + 3) % kRing);
       mask(scur, kb);
-      qk(kring + ((i + 1) & 1) * kKBytes, snext);  // last block: stale slot, unused
+      qk(kring + ((i + 1) % kRing) * kKBytes, snext);  // last block: stale slot, unused
       const float lblk = softmax(scur, pf);
       row_l += lblk;
       votes[(i & 1) * kWaves + wave] = __builtin_amdgcn_ballot_w64(!(lblk <= kGrowLimit) && lblk == lblk) != 0;
-      pv(vring + (i & 1) * kVBytes, pf);
+      pv(vring + (i % kRing) * kVBytes, pf);
       return vote_any != 0;
     };
     for (int kb = kb_begin; kb < kb_end && !aborted; kb += 2) {
@@ -284,7 +309,10 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     lds_reads_done_barrier_vm0();
     if (!aborted) {
       const int* vp = votes + ((nblk - 1) & 1) * kWaves;  // the last step's votes
-      aborted = (vp[0] | vp[1] | vp[2] | vp[3]) != 0;
+      int any = 0;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) any |= vp[v];
+      aborted = any != 0;
     }
   }
   if (aborted) {
@@ -359,7 +387,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   const int idx = blockIdx.x;
   if (idx < p.prefix_wgs) {
@@ -487,7 +515,7 @@ using namespace mm::attn;
 constexpr int kNumCUs = 256;
 // Kernel variant used by the launchers: QT q-tiles of 32 rows per wave and
 // MINB CTAs resident per CU.
-constexpr int kMinBlocks = 2;  // CTAs resident per CU
+constexpr int kMinBlocks = 1;  // CTAs resident per CU
 constexpr int kSlots = kNumCUs * kMinBlocks;
 
 // Tail KV-split cost model (re-derived from reference
