@@ -604,25 +604,47 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
   const int nparts = tbl[2 * b];
   const int rec0 = tbl[2 * b + 1];
   if (nparts <= 1) return;  // the decode kernel wrote this request's output
+  // The (m, l) pairs and O slices of up to kBatch parts are loaded together
+  // (one round of memory latency instead of one per part); the arithmetic is
+  // the same two-pass max-then-weighted-sum in part order.
+  constexpr int kBatch = 8;
   float M = -__builtin_inff();
-  for (int j = 0; j < nparts; ++j) {
-    const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
-    M = fmaxf(M, ml[rec * 2]);
+  for (int j0 = 0; j0 < nparts; j0 += kBatch) {
+    float mb[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int j = j0 + k < nparts ? j0 + k : nparts - 1;
+      mb[k] = ml[(((size_t)rec0 + j) * p.qrows + qrow) * 2];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) M = fmaxf(M, mb[k]);  // repeats of the last part change nothing
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  for (int j = 0; j < nparts; ++j) {
-    const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
-    const float m_p = ml[rec * 2];
-    const float l_p = ml[rec * 2 + 1];
-    const float diff = m_p - M;  // integer-valued or -inf, <= 0
-    const float wt = (m_p == -__builtin_inff()) ? 0.f : ((diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)diff) : 0.f);
-    const f32x4 o = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
-    acc[0] = __builtin_fmaf(wt, o[0], acc[0]);
-    acc[1] = __builtin_fmaf(wt, o[1], acc[1]);
-    acc[2] = __builtin_fmaf(wt, o[2], acc[2]);
-    acc[3] = __builtin_fmaf(wt, o[3], acc[3]);
-    L = __builtin_fmaf(wt, l_p, L);
+  for (int j0 = 0; j0 < nparts; j0 += kBatch) {
+    float mb[kBatch], lb[kBatch];
+    f32x4 ob[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int j = j0 + k < nparts ? j0 + k : nparts - 1;
+      const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
+      mb[k] = ml[rec * 2];
+      lb[k] = ml[rec * 2 + 1];
+      ob[k] = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (j0 + k < nparts) {
+        const float diff = mb[k] - M;  // integer-valued or -inf, <= 0
+        const float wt =
+            (mb[k] == -__builtin_inff()) ? 0.f : ((diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)diff) : 0.f);
+        acc[0] = __builtin_fmaf(wt, ob[k][0], acc[0]);
+        acc[1] = __builtin_fmaf(wt, ob[k][1], acc[1]);
+        acc[2] = __builtin_fmaf(wt, ob[k][2], acc[2]);
+        acc[3] = __builtin_fmaf(wt, ob[k][3], acc[3]);
+        L = __builtin_fmaf(wt, lb[k], L);
+      }
+    }
   }
   const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
   u32x2 o;
