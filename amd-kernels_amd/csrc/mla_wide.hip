@@ -116,8 +116,33 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   const int lim = S - (p.q_len - 1 - t_pos);  // tokens >= lim are masked for this row
   const long long qoff = (long long)qb * p.qrows + qr;
 
-  // Q loads go out first, ahead of the tile table and the first tiles, and are
-  // retired with them (the first segment's vmcnt(0)).
+  // Slot indices of the first staging round of the first segment (paged), then
+  // Q: the first table build waits only for the staged indices (older in the
+  // in-order vmcnt), while Q, the table build and the first tiles' gathers
+  // overlap. Staging layout: see the table build in sweep().
+  char* stg = ring + wave * (kWStageTiles * 128);
+  auto stage_round = [&](int seg_lo, int seg_hi, int ntiles, int r0) {
+    const int j0 = r0 + kWStageTiles * wave;
+    int nb = ntiles - j0;
+    nb = nb < 0 ? 0 : (nb > kWStageTiles ? kWStageTiles : nb);
+    for (int q = 0; q < (nb + 1) / 2; ++q) {
+      int tok = seg_lo + kTileTok * (j0 + 2 * q + g) + n;
+      tok = tok < seg_hi ? tok : seg_hi - 1;
+      dma4_opaque(p.kv_indices + slot0 + tok, stg + 256 * q);
+    }
+    return nb;
+  };
+  auto seg_end = [&](int seg_lo) {
+    return (long long)seg_lo + kWTabTiles * kTileTok < kv_hi ? seg_lo + kWTabTiles * kTileTok : kv_hi;
+  };
+  bool prestaged = false;
+  if constexpr (PAGED) {
+    if (kv_lo < kv_hi) {
+      const int seg_hi = seg_end(kv_lo);
+      stage_round(kv_lo, seg_hi, (seg_hi - kv_lo + kTileTok - 1) / kTileTok, 0);
+      prestaged = true;
+    }
+  }
   bf16x8 qf[2 * kQRegPairs];
 #pragma unroll
   for (int s = 0; s < kQRegPairs; ++s) {
@@ -138,6 +163,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
     const uint16_t* src = (c < 8) ? p.q_lat + ro * kLat + kQLdsDim0 + c * 8 : p.q_pe + ro * kRope + (c - 8) * 8;
     dma16_opaque(src, qlds + 1024 * it);
   }
+  constexpr int kQLoads = 2 * kQRegPairs + 8;  // vector memory ops per wave above
 
   // ---- per-lane constant offsets inside a staged tile (same layout as the 32-row kernel) ----
   const int koff0 = n * kQK + 16 * (g ^ swz(n));
@@ -184,7 +210,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   auto sweep = [&](auto max_only_tag) {
     constexpr bool kMaxOnly = decltype(max_only_tag)::value;
     for (int seg_lo = kv_lo; seg_lo < kv_hi; seg_lo += kWTabTiles * kTileTok) {
-      const int seg_hi = (long long)seg_lo + kWTabTiles * kTileTok < kv_hi ? seg_lo + kWTabTiles * kTileTok : kv_hi;
+      const int seg_hi = seg_end(seg_lo);
       const int ntiles = (seg_hi - seg_lo + kTileTok - 1) / kTileTok;
       // Every wave is done with the ring and the table (a segment's last
       // barrier already retired all of its tile DMAs).
@@ -194,17 +220,22 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
         // tokens occupy consecutive slots (one base + lane offsets), else -1.
         // Wave w stages the slot indices of tiles 64w .. 64w+63 of each round
         // of 256 in its own 8 KB of the ring (two tiles per 4-byte DMA).
-        char* stg = ring + wave * (kWStageTiles * 128);
         for (int r0 = 0; r0 < ntiles; r0 += kWWaves * kWStageTiles) {
-          const int j0 = r0 + kWStageTiles * wave;
-          int nb = ntiles - j0;
-          nb = nb < 0 ? 0 : (nb > kWStageTiles ? kWStageTiles : nb);
-          for (int q = 0; q < (nb + 1) / 2; ++q) {
-            int tok = seg_lo + kTileTok * (j0 + 2 * q + g) + n;
-            tok = tok < seg_hi ? tok : seg_hi - 1;
-            dma4_opaque(p.kv_indices + slot0 + tok, stg + 256 * q);
+          int nb;
+          if (prestaged) {
+            // First round of the first segment, staged before the Q loads:
+            // wait for it only.
+            const int j0 = kWStageTiles * wave;
+            nb = ntiles - j0;
+            nb = nb < 0 ? 0 : (nb > kWStageTiles ? kWStageTiles : nb);
+            static_assert(kQLoads == 36, "the vmcnt below counts the Q loads");
+            asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
+            prestaged = false;
+          } else {
+            nb = stage_round(seg_lo, seg_hi, ntiles, r0);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           }
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          const int j0 = r0 + kWStageTiles * wave;
           for (int q = 0; q < (nb + 1) / 2; ++q) {
             const int j = j0 + 2 * q + g;
             const int v = *reinterpret_cast<const int*>(stg + 256 * q + 4 * lane);
@@ -217,10 +248,9 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
           }
         }
       }
-      // Retire the Q loads (first segment) and the index staging, visibly to
-      // the compiler: the DMAs are invisible to its wait-count model, so a wait
-      // it placed itself before the first use of Q would also wait for tiles.
-      __builtin_amdgcn_s_waitcnt(0x0F70);
+      // Q is retired by the tile-0 wait below (it is older than the tiles); the
+      // compiler, which does not count the DMAs, adds its own wait before the
+      // first use of Q.
       if constexpr (PAGED) lds_reads_done_barrier();  // the table is complete; the staging area is free
       const int eff = lim < seg_hi ? lim : seg_hi;  // this row's token limit in the segment
 
