@@ -338,7 +338,14 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
                      "s"(pend_base), "{m0}"(m0v), "s"(pu)
                      : "memory", "scc");
       };
-      auto body = [&](int t, int pending, auto with_pv) -> f32x16 {
+      // Scores of tile t plus the PV MFMAs of tile t-1 the body carries; the
+      // operands of the 8 it leaves (k-step 1, d-tiles 2 and 3) go to finish().
+      struct Carry {
+        f32x16 s;
+        bf16x8 pop[4];
+        i32x2 v2, v3;
+      };
+      auto body = [&](int t, int pending, auto with_pv) -> Carry {
         constexpr bool kPV = decltype(with_pv)::value;
         const char* st = ring + (t & (kWSlots - 1)) * kTileBytes;          // K: tile t
         const char* sp = ring + ((t - 1) & (kWSlots - 1)) * kTileBytes;    // V: tile t-1
@@ -388,8 +395,9 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
           const bf16x8 kb = fp8x8_bf16(raw[2], raw[3]);
           s0 = mfma32(ka, qa, s0);
           if constexpr (kPV) {
-            // PV MFMA i = 2s (and 2s+1 below): k-step i/16, d-tile (i/4)%4, row tile i%4.
-            if (s < 16) {
+            // PV MFMA i = 2s (and 2s+1 below): k-step i/16, d-tile (i/4)%4, row
+            // tile i%4; i < 24 here, the last 8 run under the softmax.
+            if (s < 12) {
               const int i = 2 * s, j = (i >> 2) & 3, rt = i & 3;
               if (rt == 0) {
                 va = fp8x8_bf16((uint32_t)vraw[j][0], (uint32_t)vraw[j][1]);
@@ -402,7 +410,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
           }
           s0 = mfma32(kb, qb2, s0);
           if constexpr (kPV) {
-            if (s < 16) {
+            if (s < 12) {
               const int i = 2 * s + 1, j = (i >> 2) & 3, rt = i & 3;
               pv_mfma(oacc[4 * j + rt], va, pop[rt]);
               if (i >= 12 && i < 16) pop[rt] = *paddr(1, rt);
@@ -410,7 +418,15 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
           }
           sched_fence();
         }
-        return s0;
+        Carry cr;
+        cr.s = s0;
+        if constexpr (kPV) {
+#pragma unroll
+          for (int rt = 0; rt < 4; ++rt) cr.pop[rt] = pop[rt];
+          cr.v2 = vraw[2];
+          cr.v3 = vraw[3];
+        }
+        return cr;
       };
       // The 32 PV MFMAs of the last tile on their own.
       auto pv_last = [&](int t) {
@@ -435,23 +451,37 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
       bool pend = false;  // a deferred gather waits for the next body
       // Softmax of tile t, the tile barrier and the gather of tile t+3 (slot
       // table entry read before the barrier).
-      auto finish = [&](int t, const f32x16& sacc, int tab_next) {
+      auto finish = [&](int t, const Carry& cr, int tab_next, auto with_pv) {
+        constexpr bool kPV = decltype(with_pv)::value;
+        // The 8 PV MFMAs of tile t-1 the body left (k-step 1, d-tiles 2 and 3),
+        // one per softmax chunk below so the softmax VALU runs under them.
+        bf16x8 a2, a3;
+        if constexpr (kPV) {
+          a2 = fp8x8_bf16((uint32_t)cr.v2[0], (uint32_t)cr.v2[1]);
+          a3 = fp8x8_bf16((uint32_t)cr.v3[0], (uint32_t)cr.v3[1]);
+        }
+        auto pv_left = [&](int k) {  // k = 0..7: d-tile 2 + k/4, row tile k%4
+          if constexpr (kPV) pv_mfma(oacc[8 + k], k < 4 ? a2 : a3, cr.pop[k & 3]);
+          sched_fence();
+        };
         const int tok0 = seg_lo + t * kTileTok;
         // Lane (n, g), register i: token tok0 + 8(i/4) + 4g + i%4 of query row n.
         float sv[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sv[i] = sacc[i];
+        for (int i = 0; i < 16; ++i) sv[i] = cr.s[i];
         const int rel = eff - tok0 - 4 * g;  // register i is valid iff 8(i/4) + i%4 < rel
         if (__builtin_amdgcn_ballot_w64(rel < 32)) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) sv[i] = ((8 * (i >> 2) + (i & 3)) < rel) ? sv[i] : -__builtin_inff();
         }
+        pv_left(0);
         float mx[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) mx[i] = fmaxf(sv[i], sv[i + 8]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], mx[i + 4]);
         float bm = fmaxf(fmaxf(mx[0], mx[2]), fmaxf(mx[1], mx[3]));
+        pv_left(1);
         bm = xor32_max(bm);
         if constexpr (kMaxOnly) {
           row_m = fmaxf(row_m, bm);
@@ -464,12 +494,14 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
             grew = grew || (mc > row_m + kGrowLimit);
           }
           const float neg_m = (row_m == -__builtin_inff()) ? 0.f : -row_m;
+          pv_left(2);
           float pv[16];
           float lsum = 0.f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], c, neg_m));
             lsum += pv[i];
+            if ((i & 3) == 3) pv_left(3 + (i >> 2));  // chunks 3..6
           }
           row_l += lsum;
           // P^T operands of this row tile for both token k-steps, as the MFMA B
@@ -483,6 +515,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
                               pack2_bf16<kRTNE>(pv[8 * kk + 6], pv[8 * kk + 7])};
             *reinterpret_cast<u32x4*>(pw + 1024 * kk) = w4;
           }
+          pv_left(7);
         }
 
         // ---- tile barrier: P^T(t) published, tile t+1 landed everywhere, slot of t-1 free ----
@@ -495,18 +528,16 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
       };
       // Tile 0 has no PV before it; every later body carries the previous
       // tile's PV (one code path in the loop, so the accumulators stay put).
-      finish(0, body(0, 0, std::false_type{}), ntiles > 3 ? tab_at(3) : 0);
+      finish(0, body(0, 0, std::false_type{}), ntiles > 3 ? tab_at(3) : 0, std::false_type{});
       for (int t = 1; t < ntiles; ++t) {
         const int tab_next = (t + 3 < ntiles) ? tab_at(t + 3) : 0;
         const int pd = pend;
         pend = false;
-        f32x16 sacc;
         if constexpr (kMaxOnly) {
-          sacc = body(t, pd, std::false_type{});
+          finish(t, body(t, pd, std::false_type{}), tab_next, std::false_type{});
         } else {
-          sacc = body(t, pd, std::true_type{});
+          finish(t, body(t, pd, std::true_type{}), tab_next, std::true_type{});
         }
-        finish(t, sacc, tab_next);
       }
       if constexpr (!kMaxOnly) pv_last(ntiles - 1);
     }
