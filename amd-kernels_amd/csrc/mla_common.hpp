@@ -48,6 +48,7 @@ struct Params {
   const int* kv_indices;  // flat per-token slots (paged)
   const int* kv_indptr;   // [B+1] (paged)
   int B, H, q_len, S_fixed, parts, ngroups, paged;
+  int unit_cap;           // units one round of CTAs over the CUs holds
   int qrows;              // H * q_len
   float score_c;          // scale * kv_scale * log2(e), fp32
   float kv_scale;
@@ -85,30 +86,63 @@ __device__ __forceinline__ uint32_t u16_field(uint32_t w, int k) {
 }
 
 // ---- split plan ------------------------------------------------------------------------
-// The caller's `parts` P is a budget: with sumL the total context of the batch,
-// every request is cut into chunks of C tokens,
-//   C = max(512, roundup32(ceil(sumL / (B (P - 1)))))   (P > 1),
-// request b getting nparts_b = ceil(L_b / C) parts (at least 1). Because
-// ceil(L/C) < L/C + 1, sum_b nparts_b < sumL / C + B <= B P: the partial records
-// always fit the B * P * qrows workspace. Parts of one request have equal token
-// counts except the last, so CTAs carry similar work whatever the lengths.
+// The caller's `parts` P and the launch's unit cap (the CTAs of one round of
+// the grid over the CUs, divided by the CTAs per unit) set a budget of
+//   U = max(B, min(B * P, cap))
+// units (request parts). Every request is cut into chunks of C tokens, request
+// b getting nparts_b = max(1, ceil(L_b / C)) parts of equal size (rounded up to
+// 32 tokens; the last part takes the remainder), with C the smallest multiple
+// of 32, at least 512, for which sum_b nparts_b <= U -- found by bisection,
+// since the count only falls as C grows and C = max_b L_b gives B units. So the
+// partial records always fit the B * P * qrows workspace, one round of CTAs
+// covers the batch, and the longest part (the CTA that ends last) is as short
+// as the budget allows.
 constexpr int kMinChunk = 512;
 // The paged plan keeps three B-entry tables (12 * B bytes) in LDS scratch.
 constexpr int kMaxPagedB = 3072;  // 12 B per request: 36 KB of plan scratch
 
-__device__ __forceinline__ int chunk_tokens(long long sumL, int B, int P) {
-  if (P <= 1) return 0x7FFFFFE0;
-  long long c = (sumL + (long long)B * (P - 1) - 1) / ((long long)B * (P - 1));
-  c = (c + kTileTok - 1) / kTileTok * kTileTok;
-  if (c < kMinChunk) c = kMinChunk;
-  return c > 0x7FFFFFE0 ? 0x7FFFFFE0 : (int)c;
+// ceil(a / d) for 0 <= a, 1 <= d, a + d < 2^32.
+__device__ __forceinline__ int ceil_div_u(int a, int d) {
+  return (int)(((unsigned)a + (unsigned)d - 1u) / (unsigned)d);
 }
-__device__ __forceinline__ int nparts_of(int L, int C) { return L <= C ? 1 : (L + C - 1) / C; }
+__device__ __forceinline__ int nparts_of(int L, int C) { return L <= C ? 1 : ceil_div_u(L, C); }
 // Tokens per part of a request of L tokens in np parts: equal shares rounded up
 // to whole tiles (the last part takes the remainder).
 __device__ __forceinline__ int part_tokens(int L, int np) {
-  const int t = (L + np - 1) / np;
-  return (t + kTileTok - 1) / kTileTok * kTileTok;
+  return (ceil_div_u(L, np) + kTileTok - 1) & ~(kTileTok - 1);
+}
+__device__ __forceinline__ int unit_budget(int B, int P, int cap) {
+  const long long bp = (long long)B * (P < 1 ? 1 : P);
+  const long long m = bp < cap ? bp : cap;
+  return (int)(m > B ? m : B);
+}
+// Smallest chunk C (a multiple of 32, >= kMinChunk) with units(C) <= budget,
+// for a units(C) that is non-increasing in C with units(max L) = B <= budget.
+// Wave-uniform.
+template <class UnitsFn>
+__device__ int search_chunk(long long sumL, int maxL, int B, int budget, UnitsFn units) {
+  int hi = maxL < kMinChunk ? kMinChunk : ((maxL + kTileTok - 1) & ~(kTileTok - 1));
+  if (budget <= B) return hi;  // one part per request
+  // ceil(L / C) < L / C + 1, so C >= sumL / (budget - B) is feasible too.
+  auto ceil_div_ll = [](long long a, int d) -> long long {  // 32-bit division whenever it suffices
+    return a < 0x7FFFFFFF ? (long long)ceil_div_u((int)a, d) : (a + d - 1) / d;
+  };
+  const long long ok = ceil_div_ll(sumL, budget - B);
+  if (ok < hi) hi = ok < kMinChunk ? kMinChunk : (int)((ok + kTileTok - 1) & ~(long long)(kTileTok - 1));
+  // units(C) >= sumL / C, so C >= sumL / budget.
+  const long long need = ceil_div_ll(sumL, budget);
+  int lo = need > hi ? hi : (int)need;
+  lo = (lo + kTileTok - 1) & ~(kTileTok - 1);
+  lo = lo < kMinChunk ? kMinChunk : (lo > hi ? hi : lo);
+  while (lo < hi) {
+    const int mid = lo + ((hi - lo) / (2 * kTileTok)) * kTileTok;
+    if (units(mid) <= budget) {
+      hi = mid;
+    } else {
+      lo = mid + kTileTok;
+    }
+  }
+  return hi;
 }
 
 // Wave64 reductions and inclusive scan on DPP row shifts / broadcasts (no LDS).
@@ -141,23 +175,70 @@ struct Unit {
   int rec0;    // record part index of the request's part 0 (request-index order)
   int ptok;    // tokens per part of this request
   int units;   // total units (request parts) in the batch
+  int len;     // context length of request b
+  int slot0;   // first flat slot index of request b (paged: kv_indptr[b])
 };
 
-// Unit `u` of the batch in longest-first order: requests sorted into 16 linear
-// buckets of their part size (largest first, request index inside a bucket),
-// each request's parts consecutive. Wave-uniform, computed by one wave in
-// `scratch` (12 * B bytes of LDS that no other wave touches meanwhile).
-__device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int lane, int* scratch) {
-  int* lens = scratch;            // [B] lengths, then part sizes
+// Unit `u` of the batch. When the units fit one round of CTAs they run in
+// request order; otherwise in longest-first order: requests sorted into 16
+// linear buckets of their part size (largest first, request index inside a
+// bucket), each request's parts consecutive. Wave-uniform, computed by one wave
+// in `scratch` (12 * B bytes of LDS that no other wave touches meanwhile). The
+// first 64 lengths and kv_indptr entries are loaded in one round of latency, so
+// the unit's length and slot offset cost no further round trip for b < 64.
+__device__ Unit plan_unit_paged(const int* seq_lens, const int* kv_indptr, int B, int P, int cap, int u, int lane,
+                                int* scratch) {
+  int* lens = scratch;            // [B] lengths
   int* req_at = scratch + B;      // [B] request at each position
   int* np_at = scratch + 2 * B;   // [B] parts of the request at each position
+  const int ip0 = lane < B ? kv_indptr[lane] : 0;
+  const int l0 = lane < B ? seq_lens[lane] : 0;  // the first 64 lengths stay in a register
   long long suml = 0;
+  int maxl = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
-    const int l = (c0 + lane < B) ? seq_lens[c0 + lane] : 0;
+    const int l = c0 == 0 ? l0 : ((c0 + lane < B) ? seq_lens[c0 + lane] : 0);
     if (c0 + lane < B) lens[c0 + lane] = l;
     suml += wave_sum_i(l);  // per-chunk sums stay below 2^31 for lengths < 2^25
+    maxl = max(maxl, wave_max_i(l));
   }
-  const int C = chunk_tokens(suml, B, P);
+  auto len_at = [&](int c0) { return c0 == 0 ? l0 : ((c0 + lane < B) ? lens[c0 + lane] : 0); };
+  const int budget = unit_budget(B, P, cap);
+  const int C = search_chunk(suml, maxl, B, budget, [&](int c) {
+    int n = 0;
+    for (int c0 = 0; c0 < B; c0 += 64) n += wave_sum_i(c0 + lane < B ? nparts_of(len_at(c0), c) : 0);
+    return n;
+  });
+  if (budget <= cap) {
+    // Every unit gets a CTA of the first round, so their order does not matter:
+    // units in request order, which is also the record order (unit u of request
+    // b is record rec0(b) + part).
+    Unit r{0, 0, 1, 0, kTileTok, 0, 0, 0};
+    int run = 0;  // units of the requests before this chunk
+    bool found = false;
+    for (int c0 = 0; c0 < B; c0 += 64) {
+      const bool valid = c0 + lane < B;
+      const int l = len_at(c0);
+      const int np = valid ? nparts_of(l, C) : 0;
+      const int inc = wave_incl_scan(np);
+      const int excl = run + inc - np;
+      const unsigned long long hit = __builtin_amdgcn_ballot_w64(valid && u >= excl && u < excl + np);
+      if (!found && hit) {
+        const int hl = (int)__builtin_ctzll(hit);
+        r.b = c0 + hl;
+        r.rec0 = __builtin_amdgcn_readlane(excl, hl);
+        r.part = u - r.rec0;
+        r.nparts = __builtin_amdgcn_readlane(np, hl);
+        r.len = __builtin_amdgcn_readlane(l, hl);
+        found = true;
+      }
+      run += __builtin_amdgcn_readlane(inc, 63);
+    }
+    r.units = run;
+    r.ptok = part_tokens(r.len, r.nparts);
+    r.slot0 = r.b < 64 ? __builtin_amdgcn_readlane(ip0, r.b) : kv_indptr[r.b];
+    return r;
+  }
+  // More requests than the cap (several rounds of CTAs): longest parts first.
   int maxp = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
     const bool valid = c0 + lane < B;
@@ -166,8 +247,8 @@ __device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int la
     maxp = max(maxp, wave_max_i(pt));
   }
   maxp = __builtin_amdgcn_readfirstlane(maxp);
-  auto bucket_of = [&](int pt) {  // 0 = largest parts
-    const long long q = (long long)pt * 16 / ((long long)maxp + 1);
+  auto bucket_of = [&](int pt) {  // 0 = largest parts; pt <= maxp < 2^27
+    const unsigned q = (unsigned)pt * 16u / ((unsigned)maxp + 1u);
     return 15 - (int)q;
   };
   int start[16];
@@ -206,7 +287,7 @@ __device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int la
     }
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  Unit r{0, 0, 1, 0, kTileTok, 0};
+  Unit r{0, 0, 1, 0, kTileTok, 0, 0, 0};
   int run = 0;  // units before this chunk of positions
   bool found = false;
   for (int c0 = 0; c0 < B; c0 += 64) {
@@ -225,7 +306,9 @@ __device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int la
     run += __builtin_amdgcn_readlane(inc, 63);
   }
   r.units = run;
-  r.ptok = part_tokens(lens[r.b], r.nparts);
+  r.len = lens[r.b];
+  r.ptok = part_tokens(r.len, r.nparts);
+  r.slot0 = r.b < 64 ? __builtin_amdgcn_readlane(ip0, r.b) : kv_indptr[r.b];
   // Record offset: parts of the requests before b, in request-index order.
   int rec0 = 0;
   for (int c0 = 0; c0 < B; c0 += 64) {
@@ -234,6 +317,15 @@ __device__ Unit plan_unit_paged(const int* seq_lens, int B, int P, int u, int la
   }
   r.rec0 = rec0;
   return r;
+}
+
+// Unit `u` of a contiguous batch (every request S tokens): the same chunking,
+// units in request order.
+__device__ __forceinline__ Unit plan_unit_contig(int S, int B, int P, int cap, int u) {
+  const int C =
+      search_chunk((long long)B * S, S, B, unit_budget(B, P, cap), [&](int c) { return B * nparts_of(S, c); });
+  const int np = nparts_of(S, C);
+  return Unit{u / np, u % np, np, (u / np) * np, part_tokens(S, np), B * np, S, 0};
 }
 
 // 4-byte global -> LDS DMA (lane l's dword lands at lds_dst + 4*l), counted by
@@ -249,8 +341,10 @@ __device__ __forceinline__ void dma4_opaque(const void* gsrc, const char* lds_ds
 // V^T transpose read hit distinct LDS banks.
 __device__ __forceinline__ int swz(int t) { return (t >> 2) & 3; }
 
-// Host launcher of the 128-row kernel (mla_wide.hip); grid = CTAs.
+// Host launchers of the 128-row kernel (mla_wide.hip) and of the 16-row kernel
+// (mla_coop.hip); grid = CTAs.
 int launch_wide_kernel(const Params& p, long long grid, hipStream_t st);
+int launch_coop_kernel(const Params& p, long long grid, hipStream_t st);
 
 }  // namespace mla
 }  // namespace mm

@@ -101,11 +101,9 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   const int u = 16 * (uslot >> 1) + ((uslot & 1) ? 15 - xcd : xcd);
   Unit un;
   if constexpr (PAGED) {
-    un = plan_unit_paged(p.seq_lens, p.B, p.parts, u, lane, reinterpret_cast<int*>(wring));
+    un = plan_unit_paged(p.seq_lens, p.kv_indptr, p.B, p.parts, p.unit_cap, u, lane, reinterpret_cast<int*>(wring));
   } else {
-    const int C = chunk_tokens((long long)p.B * p.S_fixed, p.B, p.parts);
-    const int np = nparts_of(p.S_fixed, C);
-    un = Unit{u / np, u % np, np, (u / np) * np, part_tokens(p.S_fixed, np), p.B * np};
+    un = plan_unit_contig(p.S_fixed, p.B, p.parts, p.unit_cap, u);
   }
   if (u >= un.units) return;  // padding CTA (whole CTA, before any barrier)
   const int b = un.b;
@@ -115,8 +113,8 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     qb = p.rows[b];
     qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
   }
-  const int S = PAGED ? p.seq_lens[b] : p.S_fixed;
-  const int slot0 = PAGED ? p.kv_indptr[b] : 0;
+  const int S = un.len;
+  const int slot0 = un.slot0;
   const long long lo64 = (long long)part * un.ptok;
   const int kv_lo = lo64 < S ? (int)lo64 : S;
   const int kv_hi = (lo64 + un.ptok < S) ? (int)(lo64 + un.ptok) : S;
@@ -604,34 +602,27 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
   const int nparts = tbl[2 * b];
   const int rec0 = tbl[2 * b + 1];
   if (nparts <= 1) return;  // the decode kernel wrote this request's output
-  // The (m, l) pairs and O slices of up to kBatch parts are loaded together
-  // (one round of memory latency instead of one per part); the arithmetic is
-  // the same two-pass max-then-weighted-sum in part order.
+  // The (m, l) pairs and O slices of up to kBatch parts are loaded together,
+  // so a request of up to kBatch parts costs one round of memory latency after
+  // the table; the arithmetic is max-then-weighted-sum in part order.
   constexpr int kBatch = 8;
   float M = -__builtin_inff();
-  for (int j0 = 0; j0 < nparts; j0 += kBatch) {
-    float mb[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int j = j0 + k < nparts ? j0 + k : nparts - 1;
-      mb[k] = ml[(((size_t)rec0 + j) * p.qrows + qrow) * 2];
-    }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) M = fmaxf(M, mb[k]);  // repeats of the last part change nothing
-  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  for (int j0 = 0; j0 < nparts; j0 += kBatch) {
-    float mb[kBatch], lb[kBatch];
-    f32x4 ob[kBatch];
+  float mb[kBatch], lb[kBatch];
+  f32x4 ob[kBatch];
+  auto load_batch = [&](int j0) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int j = j0 + k < nparts ? j0 + k : nparts - 1;
       const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
-      mb[k] = ml[rec * 2];
-      lb[k] = ml[rec * 2 + 1];
+      const float2 m_l = *reinterpret_cast<const float2*>(ml + rec * 2);
+      mb[k] = m_l.x;
+      lb[k] = m_l.y;
       ob[k] = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
     }
+  };
+  auto accumulate = [&](int j0) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       if (j0 + k < nparts) {
@@ -644,6 +635,24 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
         acc[3] = __builtin_fmaf(wt, ob[k][3], acc[3]);
         L = __builtin_fmaf(wt, lb[k], L);
       }
+    }
+  };
+  if (nparts <= kBatch) {
+    load_batch(0);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) M = fmaxf(M, mb[k]);  // repeats of the last part change nothing
+    accumulate(0);
+  } else {
+    for (int j0 = 0; j0 < nparts; j0 += kBatch) {
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int j = j0 + k < nparts ? j0 + k : nparts - 1;
+        M = fmaxf(M, ml[(((size_t)rec0 + j) * p.qrows + qrow) * 2]);
+      }
+    }
+    for (int j0 = 0; j0 < nparts; j0 += kBatch) {
+      load_batch(j0);
+      accumulate(j0);
     }
   }
   const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
@@ -686,8 +695,13 @@ constexpr int kMaxParts = 64;
 // split records (rows x parts x 2 KB) outweigh the shared tile loads.
 constexpr int kWideMinRows = 96;
 constexpr int kWideRowsPerCta = 128;
+// Requests of at most 16 query rows run mla_coop_kernel (the 4 waves share each
+// tile: no cross-wave merge of the output).
+constexpr int kCoopMaxRows = 16;
 bool use_wide(int H, int q_len) { return H * q_len >= kWideMinRows && H * q_len <= kWideRowsPerCta; }
+bool use_coop(int H, int q_len) { return H * q_len <= kCoopMaxRows; }
 int ngroups_for(int H, int q_len) {
+  if (use_coop(H, q_len)) return 1;
   const int rows = use_wide(H, q_len) ? kWideRowsPerCta : kQRowsPerCta;
   return (H * q_len + rows - 1) / rows;
 }
@@ -700,19 +714,25 @@ int max_parts_for(int B, int H, int q_len) {
   return m < 1 ? 1 : (int)m;
 }
 
-// Split planner. The kernel cuts requests into equal chunks so that the batch
-// has about B * (parts - 1) + B/2 units (request parts), within the record
-// cap. 32-row kernel: one round of CTAs over the CUs (one CTA per CU fits in
-// LDS; per-CTA set-up dominates short CTAs). 128-row kernel: about one unit per
-// CU whatever the number of row blocks (measured: B=64, H=128, q_len 2 runs
-// 209 us with 4 parts and 448 CTAs, 264 us with 2 parts and 192 CTAs).
+// Units one round of CTAs over the CUs holds (one CTA per CU fits in LDS for
+// every kernel here; per-CTA set-up dominates short CTAs, so a second round
+// costs more than longer parts). 32-row kernel: its ngroups CTAs per unit
+// share the CUs.
+int unit_cap_for(int H, int q_len) {
+  if (use_coop(H, q_len) || use_wide(H, q_len)) return kNumCUs;
+  const int c = kNumCUs / ngroups_for(H, q_len);
+  return c < 1 ? 1 : c;
+}
+
+// Split planner: enough parts that the kernel's plan can fill the unit cap
+// (it then cuts the batch into at most min(B * parts, cap) units), within the
+// record workspace. Measured on the 128-row kernel (B=64, H=128, q_len 2):
+// 209 us with 4 parts and 448 CTAs, 264 us with 2 parts and 192 CTAs.
 int plan_parts(int B, int H, int max_seq_len, int q_len) {
   if (B < 1) B = 1;
   if (q_len < 1) q_len = 1;
-  const int ng = ngroups_for(H, q_len);
-  // Units ~ B * (p - 1) + B / 2 (see the kernel's chunking).
-  const int units = use_wide(H, q_len) ? kNumCUs : kNumCUs / ng;
-  int p = units > B / 2 ? 1 + (units - B / 2) / B : 1;
+  const int units = unit_cap_for(H, q_len);
+  int p = (units + B - 1) / B;
   const int by_len = 1 + max_seq_len / 512;  // chunks are at least 512 tokens
   if (p > by_len) p = by_len;
   const int cap = max_parts_for(B, H, q_len);
@@ -755,6 +775,7 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   p.S_fixed = S_fixed;
   p.parts = clamp_parts(parts, B, H, q_len, workspace != nullptr);
   p.ngroups = ngroups_for(H, q_len);
+  p.unit_cap = unit_cap_for(H, q_len);
   p.paged = paged ? 1 : 0;
   p.qrows = H * q_len;
   p.score_c = (float)((double)scale * (double)kv_scale * 1.4426950408889634);
@@ -766,7 +787,9 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   const long long grid = (long long)mm::kNumXcds * slots_per_xcd * p.ngroups;
   if (grid > 0x7FFFFFFFLL) return -8;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (use_wide(H, q_len))
+  if (use_coop(H, q_len))
+    launch_coop_kernel(p, grid, st);
+  else if (use_wide(H, q_len))
     launch_wide_kernel(p, grid, st);
   else if (paged)
     hipLaunchKernelGGL(mla_decode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);

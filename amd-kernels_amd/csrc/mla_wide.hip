@@ -75,7 +75,8 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   Unit un;
   if constexpr (PAGED) {
     if (wave == 0) {
-      const Unit w0 = plan_unit_paged(p.seq_lens, p.B, p.parts, u, lane, reinterpret_cast<int*>(ring));
+      const Unit w0 =
+          plan_unit_paged(p.seq_lens, p.kv_indptr, p.B, p.parts, p.unit_cap, u, lane, reinterpret_cast<int*>(ring));
       if (lane == 0) {
         misc[0] = w0.b;
         misc[1] = w0.part;
@@ -83,16 +84,17 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
         misc[3] = w0.rec0;
         misc[4] = w0.ptok;
         misc[5] = w0.units;
+        misc[6] = w0.len;
+        misc[7] = w0.slot0;
       }
     }
     lds_reads_done_barrier();
     un = Unit{__builtin_amdgcn_readfirstlane(misc[0]), __builtin_amdgcn_readfirstlane(misc[1]),
               __builtin_amdgcn_readfirstlane(misc[2]), __builtin_amdgcn_readfirstlane(misc[3]),
-              __builtin_amdgcn_readfirstlane(misc[4]), __builtin_amdgcn_readfirstlane(misc[5])};
+              __builtin_amdgcn_readfirstlane(misc[4]), __builtin_amdgcn_readfirstlane(misc[5]),
+              __builtin_amdgcn_readfirstlane(misc[6]), __builtin_amdgcn_readfirstlane(misc[7])};
   } else {
-    const int C = chunk_tokens((long long)p.B * p.S_fixed, p.B, p.parts);
-    const int np = nparts_of(p.S_fixed, C);
-    un = Unit{u / np, u % np, np, (u / np) * np, part_tokens(p.S_fixed, np), p.B * np};
+    un = plan_unit_contig(p.S_fixed, p.B, p.parts, p.unit_cap, u);
   }
   if (u >= un.units) return;  // padding CTA: every wave leaves together
   const int b = un.b;
@@ -102,8 +104,8 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
     qb = p.rows[b];
     qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
   }
-  const int S = PAGED ? p.seq_lens[b] : p.S_fixed;
-  const int slot0 = PAGED ? p.kv_indptr[b] : 0;
+  const int S = un.len;
+  const int slot0 = un.slot0;
   const long long lo64 = (long long)part * un.ptok;
   const int kv_lo = lo64 < S ? (int)lo64 : S;
   const int kv_hi = (lo64 + un.ptok < S) ? (int)(lo64 + un.ptok) : S;

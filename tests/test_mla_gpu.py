@@ -192,6 +192,81 @@ def test_wide_block_ragged_tile_edges(H, q_len, parts):
     _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
 
 
+@pytest.mark.parametrize("H,q_len,parts", [(16, 1, 1), (16, 1, 3), (8, 2, 2), (5, 3, 1), (1, 1, 2)])
+def test_small_block_ragged_tile_edges(H, q_len, parts):
+    """Query blocks of <= 16 rows run the 16-row kernel (64-token tiles, 16
+    tokens per wave): lengths at its tile and sub-tile edges, padded query
+    columns (H * q_len < 16), split parts, paged over a permuted pool."""
+    lens = [1, 5, 15, 16, 17, 31, 32, 33, 63, 64, 65, 97, 600, 1500, 2100]
+    B = len(lens)
+    pool, idx, indptr = paged_pool(lens, 69)
+    q_lat, q_pe = rand_q(B, q_len, H, 69)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    if q_len == 1:
+        ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool),
+                                      o[:, 0], _d(lens_t), None, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    else:
+        ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(lens_t), None, _d(idx),
+                                             _d(indptr), parts, SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+@pytest.mark.parametrize("H,B", [(4, 300), (64, 140)])
+def test_more_requests_than_one_round_of_ctas(H, B):
+    """More requests than one round of CTAs holds (256 for the 16-row kernel,
+    128 two-CTA units for the 32-row kernel at H=64): one part per request,
+    dispatched longest first over several rounds."""
+    lens = ragged_lens(B, 1, 300, 79)
+    pool, idx, indptr = paged_pool(lens, 79)
+    q_lat, q_pe = rand_q(B, 1, H, 79)
+    o = torch.zeros(B, 1, H, 512, dtype=torch.bfloat16, device=DEV)
+    parts = ma.mla_decode_a16w8_plan_parts_q(B, max(lens), 1, H)
+    ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool), o[:, 0],
+                                  _d(torch.tensor(lens, dtype=torch.int32)), None, _d(idx), _d(indptr), parts,
+                                  SCALE_576, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+def test_small_block_multi_segment_part():
+    """A part longer than the 16-row kernel's 32768-token tile table: the
+    second segment re-stages its slot indices and refills the ring."""
+    lens = [33100, 100]
+    B, H = len(lens), 16
+    pool, idx, indptr = paged_pool(lens, 73)
+    q_lat, q_pe = rand_q(B, 1, H, 73)
+    o = torch.zeros(B, 1, H, 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool), o[:, 0],
+                                  _d(torch.tensor(lens, dtype=torch.int32)), None, _d(idx), _d(indptr), 1, SCALE_576,
+                                  KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
+def test_small_block_bench_config_sampled():
+    """The HBM-bound shape: B=64, H=16 (128 heads over 8 GPUs), ctx ~
+    U[1024, 8192], 64-token pages; 4 sampled requests vs the oracle, and
+    run-to-run determinism."""
+    B, H = 64, 16
+    lens = ragged_lens(B, 1024, 8192, seed=5)
+    pool, idx, indptr = paged_pool(lens, 61)
+    q_lat, q_pe = rand_q(B, 1, H, 61, peak=1.0)
+    parts = ma.mla_decode_a16w8_plan_parts_q(B, 8192, 1, H)
+    o1 = torch.zeros(B, 1, H, 512, dtype=torch.bfloat16, device=DEV)
+    o2 = torch.zeros_like(o1)
+    qd, pd, lens_t = _d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(torch.tensor(lens, dtype=torch.int32))
+    pool_d, idx_d, indptr_d = _d(pool), _d(idx), _d(indptr)
+    for o in (o1, o2):
+        ma.mla_decode_a16w8_paged_dev(qd, pd, pool_d, o[:, 0], lens_t, None, idx_d, indptr_d, parts, SCALE_192,
+                                      KV_SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), "not deterministic"
+    print(_check(o1, q_lat, q_pe, fp8_bits(pool), lens, SCALE_192, kv_indices=idx.numpy(),
+                 kv_indptr=indptr.numpy(), batches=[0, 17, 40, 63]))
+
+
 @pytest.mark.parametrize("H", [16, 128])
 def test_max_fallback_on_growing_scores(H):
     """Scores that rise more than 2^64 above a row's first tile send the CTA
