@@ -45,21 +45,23 @@ constexpr int kCTileBytes = kCTileTok * kQK;            // 36864
 constexpr int kCSubBytes = kCSubTok * kQK;              // 9216
 constexpr int kCDmaPerSub = kCSubBytes / 1024;          // 9 wave-DMA instructions
 constexpr int kCSlots = 4;                              // tile ring depth
-constexpr int kCTabTiles = 512;                         // tiles per segment (32768 tokens)
 constexpr int kCQPairs = kQK / 64;                      // 9 pairs of 32-dim k-steps
 
-// LDS map (bytes).
+// LDS map (bytes). Ring slot 3 receives its first tile only after the first
+// tile barrier; before that it holds the plan scratch (wave 0), then each
+// wave's staged slot indices (9 KB per wave: 144 tiles, which bounds a segment).
 constexpr int kCRingBytes = kCSlots * kCTileBytes;              // 147456
-constexpr int kCQuarter = kCRingBytes / kCWaves;                // a wave's plan scratch / index staging
+constexpr int kCScratchOff = 3 * kCTileBytes;                   // slot 3
+constexpr int kCStageBytes = kCTileBytes / kCWaves;             // 9216 per wave
+constexpr int kCTabTiles = kCStageBytes / (kCSubTok * 4);       // 144 tiles per segment (9216 tokens)
 constexpr int kCPOff = kCRingBytes;                             // P^T of a tile: [16 rows][64 tokens] bf16
 constexpr int kCPBytes = kCRows * kCTileTok * 2;                // 2048
 constexpr int kCTabOff = kCPOff + 2 * kCPBytes;                 // 151552: [wave][kCTabTiles] first slots
-constexpr int kCMaxOff = kCTabOff + kCWaves * kCTabTiles * 4;   // 159744: [wave][16 rows] row max
-constexpr int kCLOff = kCMaxOff + kCWaves * kCRows * 4;         // 160000: [wave][16 rows] row l
-constexpr int kCMiscOff = kCLOff + kCWaves * kCRows * 4;        // 160256: fallback flags
-constexpr int kCLdsBytes = kCMiscOff + 16;                      // 160272
-static_assert(12 * kMaxPagedB <= kCQuarter, "plan scratch fits a quarter of the ring");
-static_assert(kCTabTiles * kCSubTok * 4 <= kCQuarter, "index staging fits a quarter of the ring");
+constexpr int kCMaxOff = kCTabOff + kCWaves * kCTabTiles * 4;   // 153856: [wave][16 rows] row max
+constexpr int kCLOff = kCMaxOff + kCWaves * kCRows * 4;         // 154112: [wave][16 rows] row l
+constexpr int kCMiscOff = kCLOff + kCWaves * kCRows * 4;        // 154368: unit broadcast, fallback flags
+constexpr int kCLdsBytes = kCMiscOff + 64;                      // 154432
+static_assert(12 * kMaxPagedB <= kCTileBytes, "plan scratch fits ring slot 3");
 static_assert(kCLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kCSubBytes % 1024 == 0, "a wave's share of a tile is whole DMA instructions");
 
@@ -71,20 +73,39 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 15;  // MFMA column (query row); row of A (token for QK, dim for PV)
   const int G = lane >> 4;  // 16-lane group: k-slice of the operands, 4-row slice of the result
-  char* quarter = lds + wave * kCQuarter;
+  char* stg = lds + kCScratchOff + wave * kCStageBytes;  // this wave's staged slot indices
   int* tab = reinterpret_cast<int*>(lds + kCTabOff) + wave * kCTabTiles;
   float* red_m = reinterpret_cast<float*>(lds + kCMaxOff);
   float* red_l = reinterpret_cast<float*>(lds + kCLOff);
   int* misc = reinterpret_cast<int*>(lds + kCMiscOff);
 
   // ---- work item: unit u dealt over the XCDs in snake order (as the 32-row kernel) -------
-  // Every wave plans on its own (same result, no barrier), in its own quarter of the ring.
   const int xcd = blockIdx.x % kNumXcds;
   const int uslot = blockIdx.x / kNumXcds;
   const int u = 16 * (uslot >> 1) + ((uslot & 1) ? 15 - xcd : xcd);
   Unit un;
   if constexpr (PAGED) {
-    un = plan_unit_paged(p.seq_lens, p.kv_indptr, p.B, p.parts, p.unit_cap, u, lane, reinterpret_cast<int*>(quarter));
+    // Wave 0 plans in ring slot 3 and broadcasts the unit.
+    if (wave == 0) {
+      const Unit w0 =
+          plan_unit_paged(p.seq_lens, p.kv_indptr, p.B, p.parts, p.unit_cap, u, lane,
+                          reinterpret_cast<int*>(lds + kCScratchOff));
+      if (lane == 0) {
+        misc[0] = w0.b;
+        misc[1] = w0.part;
+        misc[2] = w0.nparts;
+        misc[3] = w0.rec0;
+        misc[4] = w0.ptok;
+        misc[5] = w0.units;
+        misc[6] = w0.len;
+        misc[7] = w0.slot0;
+      }
+    }
+    lds_reads_done_barrier();
+    un = Unit{__builtin_amdgcn_readfirstlane(misc[0]), __builtin_amdgcn_readfirstlane(misc[1]),
+              __builtin_amdgcn_readfirstlane(misc[2]), __builtin_amdgcn_readfirstlane(misc[3]),
+              __builtin_amdgcn_readfirstlane(misc[4]), __builtin_amdgcn_readfirstlane(misc[5]),
+              __builtin_amdgcn_readfirstlane(misc[6]), __builtin_amdgcn_readfirstlane(misc[7])};
   } else {
     un = plan_unit_contig(p.S_fixed, p.B, p.parts, p.unit_cap, u);
   }
@@ -115,13 +136,13 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
   };
   auto ntiles_of = [&](int seg_lo, int seg_hi) { return (seg_hi - seg_lo + kCTileTok - 1) / kCTileTok; };
   // Slot indices of this wave's 16 tokens of every tile of a segment, into its
-  // quarter of the ring: one 4-byte DMA per 4 tiles (lane (G, i): tile 4q + G,
-  // token i), 256 B per DMA. Tokens past the segment re-read its last index.
+  // staging area: one 4-byte DMA per 4 tiles (lane (G, i): tile 4q + G, token
+  // i), 256 B per DMA. Tokens past the segment re-read its last index.
   auto stage = [&](int seg_lo, int seg_hi, int ntiles) {
     for (int q = 0; q < (ntiles + 3) / 4; ++q) {
       int tok = seg_lo + kCTileTok * (4 * q + G) + kCSubTok * wave + i;
       tok = tok < seg_hi ? tok : seg_hi - 1;
-      dma4_opaque(p.kv_indices + slot0 + tok, quarter + 256 * q);
+      dma4_opaque(p.kv_indices + slot0 + tok, stg + 256 * q);
     }
   };
   bool prestaged = false;
@@ -194,6 +215,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
   float row_l = 0.f;                // this lane's share of row i's sum
   bool m_fixed = false;
   bool grew = false;                // a later tile exceeded row_m by more than kGrowLimit
+  bool ring_used = false;           // a segment has run (the next one starts with a barrier)
   const float c = p.score_c;
 
   // One pass over the part. Accumulate mode: softmax + PV with each row's max
@@ -204,28 +226,50 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
     for (int seg_lo = kv_lo; seg_lo < kv_hi; seg_lo += kCTabTiles * kCTileTok) {
       const int seg_hi = seg_end(seg_lo);
       const int ntiles = ntiles_of(seg_lo, seg_hi);
+      // A later segment or pass: every wave is done with the ring and its
+      // staging area. (The first segment of the first pass needs no barrier:
+      // each wave gathers only its own sub-tiles, from its own table, into ring
+      // slots 0..2, and slot 3 -- plan scratch, staging -- takes its first tile
+      // only after the first tile barrier.)
+      if (ring_used) lds_reads_done_barrier();
+      ring_used = true;
       if constexpr (PAGED) {
         if (!prestaged) {
-          lds_reads_done_barrier();  // every wave is done with the ring
           stage(seg_lo, seg_hi, ntiles);
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         prestaged = false;
-        // Tile table: tab[j] = slot of the first token of this wave's 16 tokens
-        // of tile j when its valid tokens occupy consecutive slots, else -1.
-        for (int q = 0; q < (ntiles + 3) / 4; ++q) {
-          const int j = 4 * q + G;
-          const int v = *reinterpret_cast<const int*>(quarter + 256 * q + 4 * lane);
-          const int f0 = __builtin_amdgcn_readlane(v, 0), f1 = __builtin_amdgcn_readlane(v, 16);
-          const int f2 = __builtin_amdgcn_readlane(v, 32), f3 = __builtin_amdgcn_readlane(v, 48);
-          const int first = G == 0 ? f0 : (G == 1 ? f1 : (G == 2 ? f2 : f3));
-          const int tok = seg_lo + kCTileTok * j + kCSubTok * wave + i;
-          const unsigned long long bal = __builtin_amdgcn_ballot_w64(tok >= seg_hi || v == first + i);
-          const bool contiguous = ((bal >> (16 * G)) & 0xFFFFull) == 0xFFFFull;
-          if (i == 0 && j < ntiles) tab[j] = contiguous ? first : -1;
-        }
       }
-      lds_reads_done_barrier();  // tables complete, staging areas and the ring free
+      // Tile table of this wave: tab[j] = slot of the first of its 16 tokens of
+      // tile j when its valid tokens occupy consecutive slots, else -1. Built in
+      // batches of up to 8 staged dwords (4 tiles each), read before any table
+      // write so their LDS latencies overlap; the first batch covers the first
+      // gathers, the rest is built while they are in flight.
+      const int nq = (ntiles + 3) / 4;
+      auto build_tab = [&](int qa, int qb_end, auto batch_tag) {
+        constexpr int kB = decltype(batch_tag)::value;
+        for (int q0 = qa; q0 < qb_end; q0 += kB) {
+          int vv[kB];
+#pragma unroll
+          for (int k = 0; k < kB; ++k)
+            vv[k] = (q0 + k < qb_end) ? *reinterpret_cast<const int*>(stg + 256 * (q0 + k) + 4 * lane) : 0;
+#pragma unroll
+          for (int k = 0; k < kB; ++k) {
+            if (q0 + k < qb_end) {
+              const int v = vv[k];
+              const int j = 4 * (q0 + k) + G;
+              const int f0 = __builtin_amdgcn_readlane(v, 0), f1 = __builtin_amdgcn_readlane(v, 16);
+              const int f2 = __builtin_amdgcn_readlane(v, 32), f3 = __builtin_amdgcn_readlane(v, 48);
+              const int first = G == 0 ? f0 : (G == 1 ? f1 : (G == 2 ? f2 : f3));
+              const int tok = seg_lo + kCTileTok * j + kCSubTok * wave + i;
+              const unsigned long long bal = __builtin_amdgcn_ballot_w64(tok >= seg_hi || v == first + i);
+              const bool contiguous = ((bal >> (16 * G)) & 0xFFFFull) == 0xFFFFull;
+              if (i == 0 && j < ntiles) tab[j] = contiguous ? first : -1;
+            }
+          }
+        }
+      };
+      if constexpr (PAGED) build_tab(0, 1, std::integral_constant<int, 1>{});  // tiles 0..3
       const int eff = lim < seg_hi ? lim : seg_hi;  // this row's token limit in the segment
 
       // This wave's share of the gather of tile j into ring slot j % 4. Fast
@@ -411,6 +455,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
       issue_tile(0, tab_at(0), false);
       if (ntiles > 1) issue_tile(1, tab_at(1), false);
       if (ntiles > 2) issue_tile(2, tab_at(2), false);
+      if constexpr (PAGED) build_tab(1, nq, std::integral_constant<int, 8>{});
       // Tile 0 has no PV before it (peeled, so the accumulators stay put in the loop).
       finish(0, body(0, 0, ntiles > 2 ? 18 : (ntiles > 1 ? 9 : 0), std::false_type{}), ntiles > 3 ? tab_at(3) : 0);
       for (int t = 1; t < ntiles; ++t) {

@@ -611,15 +611,22 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
   float L = 0.f;
   float mb[kBatch], lb[kBatch];
   f32x4 ob[kBatch];
+  // Parts past the request's last are not loaded (for even qrows a workgroup's
+  // 256 cells belong to one request, so the branch is uniform).
   auto load_batch = [&](int j0) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
-      const int j = j0 + k < nparts ? j0 + k : nparts - 1;
-      const size_t rec = ((size_t)rec0 + j) * p.qrows + qrow;
-      const float2 m_l = *reinterpret_cast<const float2*>(ml + rec * 2);
-      mb[k] = m_l.x;
-      lb[k] = m_l.y;
-      ob[k] = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
+      if (j0 + k < nparts) {
+        const size_t rec = ((size_t)rec0 + j0 + k) * p.qrows + qrow;
+        const float2 m_l = *reinterpret_cast<const float2*>(ml + rec * 2);
+        mb[k] = m_l.x;
+        lb[k] = m_l.y;
+        ob[k] = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
+      } else {
+        mb[k] = -__builtin_inff();
+        lb[k] = 0.f;
+        ob[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
   };
   auto accumulate = [&](int j0) {

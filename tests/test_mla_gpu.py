@@ -231,7 +231,7 @@ def test_more_requests_than_one_round_of_ctas(H, B):
 
 
 def test_small_block_multi_segment_part():
-    """A part longer than the 16-row kernel's 32768-token tile table: the
+    """A part longer than the 16-row kernel's 9216-token tile table: the
     second segment re-stages its slot indices and refills the ring."""
     lens = [33100, 100]
     B, H = len(lens), 16
