@@ -452,12 +452,14 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
         pend = (t + 3 < ntiles) ? issue_tile(t + 3, tab_next, true) : false;
       };
 
+      // Tiles 0 and 1 now; a fast-path tile 2 goes out one DMA per step of
+      // body(0) (108 back-to-back DMAs per CU stall the issuing waves for ~1 us).
       issue_tile(0, tab_at(0), false);
       if (ntiles > 1) issue_tile(1, tab_at(1), false);
-      if (ntiles > 2) issue_tile(2, tab_at(2), false);
+      const bool pend0 = (ntiles > 2) ? issue_tile(2, tab_at(2), true) : false;
       if constexpr (PAGED) build_tab(1, nq, std::integral_constant<int, 8>{});
       // Tile 0 has no PV before it (peeled, so the accumulators stay put in the loop).
-      finish(0, body(0, 0, ntiles > 2 ? 18 : (ntiles > 1 ? 9 : 0), std::false_type{}), ntiles > 3 ? tab_at(3) : 0);
+      finish(0, body(0, pend0, ntiles > 1 ? 9 : 0, std::false_type{}), ntiles > 3 ? tab_at(3) : 0);
       for (int t = 1; t < ntiles; ++t) {
         const int tab_next = (t + 3 < ntiles) ? tab_at(t + 3) : 0;
         const int pd = pend;
