@@ -1,7 +1,7 @@
-// Shared pieces of the gfx950 absorbed-MLA decode kernels (mla_decode.hip:
-// 32 query rows per CTA; mla_wide.hip: 128 query rows per CTA): the fused fp8
-// row format, launch parameters, exact fp8 -> bf16 widening, and the device-side
-// split plan both kernels deal their units from.
+// Shared pieces of the gfx950 absorbed-MLA decode kernels (mla_coop.hip: up
+// to 16 query rows per CTA; mla_decode.hip: 32; mla_wide.hip: 128): the fused
+// fp8 row format, launch parameters, exact fp8 -> bf16 widening, and the
+// device-side split plan the kernels deal their units from.
 #pragma once
 
 #include <hip/hip_runtime.h>
