@@ -31,11 +31,13 @@
 //  * The 4 waves' (O, m, l) are merged through LDS, each wave finalising 4 of
 //    the 16 d-tiles. Split-KV parts > 1 write unnormalised fp32 (O, m, l)
 //    records that mla_merge_kernel combines with power-of-two weights.
-//  * Work split: the caller's parts budget P fixes a chunk size C from the
-//    batch's total context (read on the device from seq_lens), each request is
-//    cut into ceil(L / C) equal parts, and the units (request parts, longest
-//    first) are dealt in snake order over the 8 XCDs, so CTAs carry similar
-//    work whatever the length mix.
+//  * Work split (plan_unit_paged, shared with the other two kernels): the
+//    caller's parts budget and one round of CTAs over the CUs bound the number
+//    of units (request parts); the device picks the smallest chunk C whose
+//    units fit, from the batch's lengths read on the device, and cuts each
+//    request into ceil(L / C) equal parts. Units run in request order when they
+//    fit one round, otherwise longest first; they are dealt in snake order over
+//    the 8 XCDs.
 //  * Paged gathers: each wave stages its tiles' slot indices and keeps, per
 //    tile, the first slot when the tile's tokens occupy consecutive slots (one
 //    SGPR base + per-lane offsets per DMA); any other tile is gathered row by
@@ -90,10 +92,10 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
 
   // ---- work item ----------------------------------------------------------------------
   // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8) and in
-  // blockIdx order within an XCD. Units (request parts, longest first) are dealt
-  // to XCDs in snake order (XCD x takes units x, 15-x, 16+x, 31-x, ...) so every
-  // XCD gets a similar share and starts with its longest units; the ngroups CTAs
-  // of a unit run on one XCD (its KV is shared through that L2).
+  // blockIdx order within an XCD. Units are dealt to XCDs in snake order (XCD x
+  // takes units x, 15-x, 16+x, 31-x, ...) so every XCD gets a similar share
+  // (and, when units are ordered longest first, starts with its longest); the
+  // ngroups CTAs of a unit run on one XCD (its KV is shared through that L2).
   const int xcd = blockIdx.x % kNumXcds;
   const int k_in_xcd = blockIdx.x / kNumXcds;
   const int uslot = k_in_xcd / p.ngroups;

@@ -176,20 +176,49 @@ def test_mla_checks_without_device():
         _check_q(q, _bf16(2, 1, 16, 64), _bf16(2, 16, 512), "x", multiq=False)
 
 
+def _mla_units(lens, c):
+    return sum(1 if L <= c else -(-L // c) for L in lens)
+
+
+def _mla_search_chunk(lens, budget):
+    """csrc/mla_common.hpp search_chunk: bisection between sumL / budget and the
+    feasible sumL / (budget - B) (or max L) over multiples of 32, >= 512."""
+    B, sumL, maxL = len(lens), sum(lens), max(lens)
+    hi = 512 if maxL < 512 else -(-maxL // 32) * 32
+    if budget <= B:
+        return hi
+    ok = -(-sumL // (budget - B))
+    if ok < hi:
+        hi = 512 if ok < 512 else -(-ok // 32) * 32
+    lo = min(-(-sumL // budget), hi)
+    lo = max(512, min(-(-lo // 32) * 32, hi))
+    while lo < hi:
+        mid = lo + ((hi - lo) // 64) * 32
+        if _mla_units(lens, mid) <= budget:
+            hi = mid
+        else:
+            lo = mid + 32
+    return hi
+
+
 def test_mla_split_plan_fits_workspace():
-    """The device split plan (chunk C = max(512, roundup32(ceil(sumL / (B (P-1))))),
-    ceil(L_b / C) parts per request) never needs more than B * P records, for
-    random and adversarial length mixes; mirrors csrc/mla_decode.hip chunk_tokens."""
+    """The device split plan (budget U = max(B, min(B * P, cap)) units; chunk C =
+    the smallest multiple of 32, >= 512, with sum_b max(1, ceil(L_b / C)) <= U)
+    never needs more than B * P records and is minimal, for random and
+    adversarial length mixes and the kernels' caps (256 CUs / CTAs per unit)."""
     import numpy as np
 
     rng = np.random.default_rng(3)
     cases = [rng.integers(0, 9000, size=int(rng.integers(1, 200))).tolist() for _ in range(300)]
-    cases += [[0] * 7, [1] * 64, [100000] + [1] * 63, [512] * 10, [513] * 10]
+    cases += [[0] * 7, [1] * 64, [100000] + [1] * 63, [512] * 10, [513] * 10, [8192] * 64]
     for lens in cases:
         B = len(lens)
-        for P in (2, 3, 4, 8, 16):
-            sumL = sum(lens)
-            c = -(-sumL // (B * (P - 1)))
-            c = max(512, -(-c // 32) * 32)
-            total = sum(1 if L <= c else -(-L // c) for L in lens)
-            assert total <= B * P, (lens, P, total)
+        for P in (1, 2, 3, 4, 8, 16):
+            for cap in (256, 128, 32):
+                budget = max(B, min(B * P, cap))
+                c = _mla_search_chunk(lens, budget)
+                total = _mla_units(lens, c)
+                assert c % 32 == 0 and c >= 512, (lens, P, cap, c)
+                assert total <= budget <= max(B, B * P), (lens, P, cap, total)
+                # minimal: 32 tokens less no longer fits (or the 512 floor)
+                assert c == 512 or _mla_units(lens, c - 32) > budget, (lens, P, cap, c)
