@@ -292,7 +292,25 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       int vote_any = 0;
 #pragma unroll
       for (int v = 0; v < kWaves; ++v) vote_any |= vp[v];
-      if (i + 3 < nblk) issue_kv(kb + 3, (i + 3) % kRing);
+      // Block kb+3: a full block's 4 DMAs go out one per odd QK step below (all
+      // 8 waves issuing theirs back to back after the barrier stall their QK);
+      // a partial last block is gathered here.
+      const bool dma3 = i + 3 < nblk;
+      const bool dma3_full = dma3 && (kb + 4) * kKvBlock <= p.Skv;
+      if (dma3 && !dma3_full) issue_kv(kb + 3, (i + 3) % kRing);
+      const int pd3 = __builtin_amdgcn_readfirstlane((int)dma3_full);
+      const char* kbase3 = kh + (long long)(kb + 3) * kblk_bytes;
+      const char* vbase3 = vth + (long long)(kb + 3) * kVBytes;
+      const char* kst3 = kring + ((i + 3) % kRing) * kKBytes;
+      const char* vst3 = vring + ((i + 3) % kRing) * kVBytes;
+      auto dma3_step = [&](int d) {  // d = 0, 1: K instructions; 2, 3: V instructions
+        const char* src = d < 2 ? kbase3 + koff[d] : vbase3 + voff + (d - 2) * kFragBytes;
+        const char* dst = d < 2 ? kst3 + (wave * 2 + d) * kFragBytes : vst3 + (wave * 2 + d - 2) * kFragBytes;
+        const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)dst;
+        asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\tglobal_load_lds_dwordx4 %0, off\n1:" ::"v"(src),
+                     "{m0}"(m0v), "s"(pd3)
+                     : "memory", "scc");
+      };
       mask(scur, kb);
       // Sliced pipeline: QK(i+1) (16 MFMAs) carries softmax(i) of row tile 0
       // and the first half of row tile 1; PV(i) of row tile 0 (8 MFMAs) carries
@@ -340,6 +358,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         }
         snext[0] = mfma32(kf0, qf[ds], snext[0]);
         sm_pair(0, ds);
+        if (ds & 1) dma3_step(ds >> 1);
         snext[1] = mfma32(kf1, qf[ds], snext[1]);
         if (ds & 1) sm_pair(1, ds >> 1);
         if (ds + 1 < 8) {
