@@ -42,7 +42,7 @@ constexpr int kKvBlock = 64;       // kv rows per main-loop block
 constexpr int kWaves = 8;          // waves per CTA (two per SIMD; one CTA per CU)
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQRowsPerTile = 32;  // q rows per wave = one 32x32 MFMA tile
-constexpr int kRowsPerCta = kWaves * kQRowsPerTile;  // 128
+constexpr int kRowsPerCta = kWaves * kQRowsPerTile;  // 256
 constexpr int kFragBytes = 1024;   // one 32x16 bf16 MFMA operand fragment (64 lanes x 16 B)
 constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
 constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
@@ -114,7 +114,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   const float c = p.scale_log2e;
   const int kv_end = p.Skv < kb_end * kKvBlock ? p.Skv : kb_end * kKvBlock;
 
-  // LDS: K ring [2] | V_t ring [2] | abort votes.
+  // LDS: K ring [kRing] | V_t ring [kRing] | abort votes [2][kWaves].
   // K slot: row-major [64 rows][256 B], the 16-byte chunk c of row k stored at
   // chunk position c ^ (k & 15): one DMA instruction moves 4 whole rows
   // (coalesced 256-byte reads) and the MFMA fragment reads are conflict free.
