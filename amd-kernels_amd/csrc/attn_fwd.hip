@@ -562,43 +562,47 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(Params p, int
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
                                                           int H, int Skv, int nkb, int bshd) {
-  __shared__ uint16_t tile[kKvBlock][kD + 2];
+  // Row-major tile of the block's 64 rows, 288-byte row pitch (256 B + 32 B of
+  // padding: the four rows of one transposing read start 8 banks apart).
+  constexpr int kPitch = 288;
+  __shared__ __attribute__((aligned(16))) char tile[kKvBlock * kPitch];
   const int kb = blockIdx.x % nkb;
   const int bh = blockIdx.x / nkb;
   const int b = bh / H, h = bh % H;
   const long long row_stride = bshd ? (long long)H * kD : kD;
   const uint16_t* vh = v + head_base(b, h, Skv, H, bshd);
   const int tid = threadIdx.x;
-  // Load 64 rows x 256 B: 1024 16-byte pieces, 4 per thread.
+  // Load 64 rows x 256 B: 1024 16-byte pieces, 4 per thread, one LDS write each.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int piece = tid + i * 256;
-    const int row = piece >> 4, col = (piece & 15) * 8;
+    const int row = piece >> 4, c16 = piece & 15;
     const int kv = kb * kKvBlock + row;
     u32x4 val = {0u, 0u, 0u, 0u};
-    if (kv < Skv) val = *reinterpret_cast<const u32x4*>(vh + (long long)kv * row_stride + col);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      tile[row][col + 2 * e] = (uint16_t)(val[e] & 0xFFFFu);
-      tile[row][col + 2 * e + 1] = (uint16_t)(val[e] >> 16);
-    }
+    if (kv < Skv) val = *reinterpret_cast<const u32x4*>(vh + (long long)kv * row_stride + c16 * 8);
+    *reinterpret_cast<u32x4*>(tile + row * kPitch + c16 * 16) = val;
   }
   __syncthreads();
+  // Output unit (fragment f, lane l): 8 bf16 of column d = 32dt + l%32, rows
+  // base + {0..3, 8..11} with base = 32t + 16s + 4(l/32). A 16-lane group holds
+  // 16 consecutive columns d0 .. d0+15 of one base, so two ds_read_b64_tr_b16
+  // (within a 16-lane group out[i][e] = in[4e + i/4][i%4]) deliver them: member
+  // m supplies 4 bf16 of row base(+8) + m/4 at columns d0 + 4(m%4), and lane i
+  // receives column d0 + i of those 4 rows.
   uint16_t* dst = vt + ((long long)bh * nkb + kb) * kVtBlockElems;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int unit = tid + i * 256;  // (fragment, lane)
+    const int unit = tid + i * 256;
     const int f = unit >> 6, lane = unit & 63;
     const int t = f >> 3, s = (f >> 2) & 1, dt = f & 3;
-    const int gg = lane >> 5, d = dt * 32 + (lane & 31);
-    u32x4 out;
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      const int ea = 2 * e2, eb = 2 * e2 + 1;
-      const int kva = t * 32 + s * 16 + (ea >> 2) * 8 + gg * 4 + (ea & 3);
-      const int kvb = t * 32 + s * 16 + (eb >> 2) * 8 + gg * 4 + (eb & 3);
-      out[e2] = (uint32_t)tile[kva][d] | ((uint32_t)tile[kvb][d] << 16);
-    }
+    const int base = t * 32 + s * 16 + (lane >> 5) * 4;
+    const int d0 = dt * 32 + ((lane >> 4) & 1) * 16;
+    const int m = lane & 15;
+    const char* a = tile + (base + (m >> 2)) * kPitch + (d0 + 4 * (m & 3)) * 2;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MM_LDS i16x4*)a);
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MM_LDS i16x4*)(a + 8 * kPitch));
+    const u32x2 lo2 = __builtin_bit_cast(u32x2, lo), hi2 = __builtin_bit_cast(u32x2, hi);
+    const u32x4 out = {lo2[0], lo2[1], hi2[0], hi2[1]};
     *reinterpret_cast<u32x4*>(dst + (size_t)unit * 8) = out;
   }
 }
