@@ -699,9 +699,11 @@ constexpr int kMaxParts = 64;
 
 // Requests of 96..128 query rows (H * q_len) run mla_wide_kernel (one 128-row
 // block per CTA); others the 32-row kernel. Measured at B=64, ctx U[1024,8192]
-// (steady clocks): H=128 q_len 1: 118 us wide vs 132 us 32-row; H=128 q_len 2
-// (two row blocks): 213 us wide vs 185 us 32-row -- with several row blocks the
-// split records (rows x parts x 2 KB) outweigh the shared tile loads.
+// (steady clocks): H=128 q_len 1: 108 us wide (4 parts) vs 131 us 32-row
+// unsplit, 120-124 us 32-row with 2 parts (two rounds of CTAs, in request or
+// longest-first order) and 149-153 us with 4 parts; H=128 q_len 2 (two row
+// blocks): 213 us wide vs 185 us 32-row -- with several row blocks the split
+// records (rows x parts x 2 KB) outweigh the shared tile loads.
 constexpr int kWideMinRows = 96;
 constexpr int kWideRowsPerCta = 128;
 // Requests of at most 16 query rows run mla_coop_kernel (the 4 waves share each
