@@ -48,9 +48,11 @@ constexpr int kKBytes = kKvBlock * kD * 2;   // 16 KB per K block
 constexpr int kVBytes = kKvBlock * kD * 2;   // 16 KB per V_t block
 constexpr int kVtBlockElems = kKvBlock * kD; // 8192 bf16 per V_t block
 constexpr int kRing = 4;           // K / V_t ring slots: block j lives in slot j % kRing
-constexpr int kLdsBytes = kRing * (kKBytes + kVBytes) + 2 * kWaves * 4;  // rings + votes [2][kWaves]
-// Pass 0 accepts blocks whose per-lane sum of p stays <= 2^kGrowLog2, which
-// bounds every p by that value (no fp32 overflow of O for |v| < 2^90).
+constexpr int kLdsBytes = kRing * (kKBytes + kVBytes);  // K ring + V_t ring
+// A row's running max m stays fixed while every p = 2^(s*c - m) of a block
+// stays <= kGrowLimit (tested on the lane's sums of 8 p, which bound each p).
+// A larger p makes the wave raise m and rescale (see rebase in run_tile), so O
+// and l never hold a p above 2^20 (no fp32 overflow of O for |v| < 2^90).
 constexpr float kGrowLimit = 1048576.0f;     // 2^20
 
 // Split-KV limits: partial records are laid out for CTAs of kMaxRows q rows
@@ -88,15 +90,16 @@ __device__ __forceinline__ long long head_base(int b, int h, int S, int H, int b
 // the headline shape: 1.485 ms vs 1.621 ms for two 128-row CTAs per CU with
 // 2-slot rings and one block of lead).
 //
-// Max policy: the running max m is an integer (log2 units) and is FIXED for the
-// main pass over the kv range, so O and l are never rescaled in the loop:
-// m = ceil(max of the first block) per row, and later blocks are accepted while
-// the lane's per-block sum of p stays <= kGrowLimit. If any row exceeds it the
-// waves vote through LDS and the CTA re-walks the range with an eager
-// integer-grid running max (rescales by exact powers of two). Since m is always
-// an integer, bf16(P) under any such m equals bf16(P) under the final max times
-// an exact power of two: the output does not depend on the path taken, the KV
-// blocking or the split.
+// Max policy: each row's running max m is an integer (log2 units), set from
+// the first block (m = ceil(max(s) * c)) and kept while the block's p stay
+// <= kGrowLimit, so O and l are not rescaled in the common case. A block with
+// a larger p makes its wave (a wave owns its rows, so no other wave takes
+// part) raise m to the integer ceiling of the block's max, scale O and l by
+// the exact power of two 2^(m_old - m_new) and recompute the block's p before
+// they reach PV. Since m is always an integer, bf16(P) under any such m is
+// bf16(P) under the final max times an exact power of two (up to the last
+// fp32 bit of the exp2 argument): the output does not depend on where the
+// rebases happen, on the KV blocking or on the split.
 template <int MODE>
 __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb_begin, int kb_end, int part,
                                          char* lds) {
@@ -114,14 +117,13 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   const float c = p.scale_log2e;
   const int kv_end = p.Skv < kb_end * kKvBlock ? p.Skv : kb_end * kKvBlock;
 
-  // LDS: K ring [kRing] | V_t ring [kRing] | abort votes [2][kWaves].
+  // LDS: K ring [kRing] | V_t ring [kRing].
   // K slot: row-major [64 rows][256 B], the 16-byte chunk c of row k stored at
   // chunk position c ^ (k & 15): one DMA instruction moves 4 whole rows
   // (coalesced 256-byte reads) and the MFMA fragment reads are conflict free.
   // V_t slot: fragments [t(2)][s(2)][dt(4)], 1 KB each in lane order.
   char* kring = lds;
   char* vring = lds + kRing * kKBytes;
-  int* votes = reinterpret_cast<int*>(lds + kRing * (kKBytes + kVBytes));
   // Lane byte offsets of this wave's 2 K-DMA instructions within a block (16
   // instructions of 4 rows each per block, 2 per wave).
   uint32_t koff[2];
@@ -183,20 +185,6 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     }
   };
   f32x16 oacc[4];
-  auto pv = [&](const char* vst, const bf16x8 (&pp)[2][2]) {
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16x8 vf =
-              *reinterpret_cast<const bf16x8*>(vst + ((t * 2 + s) * 4 + dt) * kFragBytes + lane * 16);
-          oacc[dt] = mfma32(vf, pp[t][s], oacc[dt]);
-        }
-      }
-    }
-  };
   // Rows past kv_end get -inf scores (p = 0). Uniform branch: last block only.
   auto mask = [&](f32x16 (&s)[2], int kb) {
     const int kv0 = kb * kKvBlock;
@@ -210,49 +198,24 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         }
     }
   };
-  auto block_max = [&](const f32x16 (&s)[2]) {
+  // Integer-grid max of row tiles t0..1 of a block: ceil(max(s) * c), NaN
+  // ignored (fmaxf), -inf when every score is -inf or NaN.
+  auto block_max = [&](const f32x16 (&s)[2], int t0) {
     float bm = -__builtin_inff();
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = t0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e) bm = fmaxf(bm, s[t][e]);
     return __builtin_ceilf(xor32_max(bm) * c);
   };
   float row_m = kNegFltMax, row_l = 0.f;
-  // p = 2^(s*c - m) -> bf16 P (per mode) for the PV B operand; returns the
-  // lane's fp32 sum of p over the block.
-  auto softmax = [&](const f32x16 (&s)[2], bf16x8 (&pp)[2][2]) {
-    const float neg_m = -row_m;
-    float lpart[4];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        uint32_t w[4];
-        float acc = 0.f;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * ss + 2 * e2], c, neg_m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * ss + 2 * e2 + 1], c, neg_m));
-          acc += p0 + p1;
-          w[e2] = pack2_bf16<MODE>(p0, p1);
-        }
-        lpart[t * 2 + ss] = acc;
-        u32x4 wv = {w[0], w[1], w[2], w[3]};
-        pp[t][ss] = __builtin_bit_cast(bf16x8, wv);
-      }
-    }
-    return (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
-  };
 
   f32x16 sA[2], sB[2];
   bf16x8 pf[2][2];
   const int nblk = kb_end - kb_begin;
-  bool aborted = false;
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
-    if (tid < 2 * kWaves) votes[tid] = 0;
     // Blocks 0..2 in flight; block j lives in slot j % kRing.
     auto issue_kv = [&](int kb, int slot) {
       issue_k(kb, slot);
@@ -271,9 +234,8 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     }
     qk(kring, sA);
     mask(sA, kb_begin);
-    row_m = fmaxf(block_max(sA), kNegFltMax);
+    row_m = fmaxf(block_max(sA, 0), kNegFltMax);
 
-    // One block: returns true when some wave voted to abort (seen one block late).
     auto step = [&](int kb, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
       const int i = kb - kb_begin;
       // Block i+1 has landed (block i+2 stays in flight, 4 DMAs per wave); every
@@ -285,13 +247,6 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       }
       sched_fence();
-      // Votes are double-buffered by step parity: step i reads exactly step
-      // i - 1's votes (written before this barrier), never a faster wave's
-      // vote of step i, so every wave takes the same abort decision.
-      const int* vp = votes + ((i + 1) & 1) * kWaves;
-      int vote_any = 0;
-#pragma unroll
-      for (int v = 0; v < kWaves; ++v) vote_any |= vp[v];
       // Block kb+3: a full block's 4 DMAs go out one per odd QK step below (all
       // 8 waves issuing theirs back to back after the barrier stall their QK);
       // a partial last block is gathered here.
@@ -315,18 +270,56 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // Sliced pipeline: QK(i+1) (16 MFMAs) carries softmax(i) of row tile 0
       // and the first half of row tile 1; PV(i) of row tile 0 (8 MFMAs) carries
       // the rest; PV(i) of row tile 1 follows. Per-accumulator orders (S, O and
-      // each lpart sum) are those of the unsliced softmax / pv: bit-identical.
+      // each lpart sum) are those of an unsliced softmax.
       const char* kst = kring + ((i + 1) % kRing) * kKBytes;  // last block: stale slot, unused
       const char* vst = vring + (i % kRing) * kVBytes;
-      const float neg_m = -row_m;
+      const float neg_m0 = -row_m;
       float lpart[4] = {0.f, 0.f, 0.f, 0.f};
       uint32_t w[2][2][4];
-      auto sm_pair = [&](int t, int pi) {
+      // p of score pair pi (0..7) of row tile t, under the running max -neg_m.
+      auto sm_pair = [&](int t, int pi, float neg_m) {
         const int ss = pi >> 2, e2 = pi & 3;
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(scur[t][8 * ss + 2 * e2], c, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(scur[t][8 * ss + 2 * e2 + 1], c, neg_m));
         lpart[t * 2 + ss] += p0 + p1;
         w[t][ss][e2] = pack2_bf16<MODE>(p0, p1);
+      };
+      auto pack_pf = [&](int t) {
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+          const u32x4 wv = {w[t][ss][0], w[t][ss][1], w[t][ss][2], w[t][ss][3]};
+          pf[t][ss] = __builtin_bit_cast(bf16x8, wv);
+        }
+      };
+      // Some lane of the wave has a p above kGrowLimit in score halves
+      // [h0, h1) (half hh = row tile hh / 2, pairs 4 (hh % 2) .. +3; halves below
+      // h0 are accepted, and those of earlier blocks are in O): raise each row's
+      // max to cover halves [h0, h1), rescale O, l and the accepted half sums
+      // by the exact power of two 2^(m_old - m_new), and recompute the p of
+      // halves [h0, h1).
+      auto rebase = [&](int h0, int h1) {
+        float bm = -__builtin_inff();
+#pragma unroll
+        for (int hh = h0; hh < h1; ++hh)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) bm = fmaxf(bm, scur[hh >> 1][8 * (hh & 1) + e]);
+        const float m_new = fmaxf(row_m, __builtin_ceilf(xor32_max(bm) * c));
+        const float diff = row_m - m_new;  // integer-valued <= 0, -inf or NaN (both +inf)
+        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
+        sc = (diff >= -126.f) ? sc : 0.f;
+        sc = (m_new > row_m) ? sc : 1.f;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= sc;
+        row_l *= sc;
+#pragma unroll
+        for (int hh = 0; hh < h0; ++hh) lpart[hh] *= sc;
+        row_m = m_new;
+#pragma unroll
+        for (int hh = h0; hh < h1; ++hh) {
+          lpart[hh] = 0.f;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) sm_pair(hh >> 1, 4 * (hh & 1) + e2, -m_new);
+        }
       };
       auto kfrag = [&](int t, int ds) {
         const int row = t * 32 + r;
@@ -357,22 +350,25 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
           for (int k = 0; k < 4; ++k) vb[k] = vfrag_n(k);
         }
         snext[0] = mfma32(kf0, qf[ds], snext[0]);
-        sm_pair(0, ds);
+        sm_pair(0, ds, neg_m0);
         if (ds & 1) dma3_step(ds >> 1);
         snext[1] = mfma32(kf1, qf[ds], snext[1]);
-        if (ds & 1) sm_pair(1, ds >> 1);
+        if (ds & 1) sm_pair(1, ds >> 1, neg_m0);
         if (ds + 1 < 8) {
           kf0 = nk0;
           kf1 = nk1;
         }
         sched_fence();
       }
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const u32x4 wv = {w[0][ss][0], w[0][ss][1], w[0][ss][2], w[0][ss][3]};
-        pf[0][ss] = __builtin_bit_cast(bf16x8, wv);
-      }
+      pack_pf(0);
       __builtin_amdgcn_s_setprio(0);
+      // Wave-uniform growth tests: row tile 0 and the first half of row tile 1
+      // before any PV of this block, the second half of row tile 1 before its PV.
+      if (__builtin_amdgcn_ballot_w64(fmaxf(lpart[0] + lpart[1], lpart[2]) > kGrowLimit) != 0) {
+        rebase(0, 3);
+        pack_pf(0);
+      }
+      const float neg_m1 = -row_m;
       // PV of row tile 0 (k-step ss, d-tile dt) with softmax pairs 4..7 of tile 1.
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
@@ -380,17 +376,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         const bf16x8 a = vb[m & 3];
         vb[m & 3] = vfrag_n(m + 4);
         oacc[dt] = mfma32(a, pf[0][ss], oacc[dt]);
-        if (m < 4) sm_pair(1, 4 + m);
+        if (m < 4) sm_pair(1, 4 + m, neg_m1);
         sched_fence();
       }
-#pragma unroll
-      for (int ss = 0; ss < 2; ++ss) {
-        const u32x4 wv = {w[1][ss][0], w[1][ss][1], w[1][ss][2], w[1][ss][3]};
-        pf[1][ss] = __builtin_bit_cast(bf16x8, wv);
-      }
-      const float lblk = (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
-      row_l += lblk;
-      votes[(i & 1) * kWaves + wave] = __builtin_amdgcn_ballot_w64(!(lblk <= kGrowLimit) && lblk == lblk) != 0;
+      if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
+      pack_pf(1);
       // PV of row tile 1.
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
@@ -399,49 +389,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         if (m + 4 < 8) vb[m & 3] = vfrag_n(8 + m + 4);
         oacc[dt] = mfma32(a, pf[1][ss], oacc[dt]);
       }
-      return vote_any != 0;
+      row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
     };
-    for (int kb = kb_begin; kb < kb_end && !aborted; kb += 2) {
-      aborted = step(kb, sA, sB);
-      if (!aborted && kb + 1 < kb_end) aborted = step(kb + 1, sB, sA);
-    }
-    sched_fence();
-    lds_reads_done_barrier_vm0();
-    if (!aborted) {
-      const int* vp = votes + ((nblk - 1) & 1) * kWaves;  // the last step's votes
-      int any = 0;
-#pragma unroll
-      for (int v = 0; v < kWaves; ++v) any |= vp[v];
-      aborted = any != 0;
-    }
-  }
-  if (aborted) {
-    // Fallback for rows whose max grew past kGrowLimit: walk the range again
-    // with an eager integer-grid running max; each raise rescales O and l by
-    // an exact power of two.
-    row_m = kNegFltMax;
-    row_l = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
-      lds_reads_done_barrier_vm0();
-      issue_k(kb, 0);
-      issue_v(kb, 0);
-      wait_vmem_barrier<0>();
-      qk(kring, sA);
-      mask(sA, kb);
-      const float m_new = fmaxf(row_m, block_max(sA));
-      if (m_new > row_m) {
-        const float diff = row_m - m_new;  // integer-valued, < 0
-        float sc = __builtin_ldexpf(1.0f, (int)fmaxf(diff, -127.f));
-        sc = (diff >= -126.f) ? sc : 0.f;
-        row_l *= sc;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= sc;
-        row_m = m_new;
-      }
-      row_l += softmax(sA, pf);
-      pv(vring, pf);
+    for (int kb = kb_begin; kb < kb_end; kb += 2) {
+      step(kb, sA, sB);
+      if (kb + 1 < kb_end) step(kb + 1, sB, sA);
     }
   }
   sched_fence();

@@ -8,9 +8,12 @@ forward kernel, as the reference times it, benchmark/runner.py:176-181).
 
 ``roofline`` is for the dominant kernel (the attention forward kernel alone,
 timed with HIP events on the stream it is launched on). ``cpu_baseline`` times
-the reference repo's CPU oracle formula (examples/basic.py:16-17) on a bounded
-sample of heads on this host's cores. ``mla`` carries the MLA decode line
-(HBM GB/s) when the MLA kernel is built.
+the reference repo's CPU oracle formula (examples/basic.py:16-17) over the
+whole headline workload on this host's cores (median of 3). Extra keys:
+``attention`` (every round mode, the reference benchmark's "realistic" inputs,
+the configs[3] long shapes, a shape whose tail KV-split fires, with and
+without the split) and ``mla`` (configs[4] decode lines with their own CPU
+baseline, the reference test's fp32 formula).
 """
 import argparse
 import json
@@ -53,24 +56,38 @@ def _warm(torch, fn, calls):
     torch.cuda.synchronize()
 
 
-def bench_attention(args, torch, ma, _lib):
-    B, S, H = 2, 8192, 24
-    mode = args.mode
-    g = torch.Generator().manual_seed(42)
-    q, k, v = (torch.randn(B, S, H, 128, generator=g).to(torch.bfloat16).to("cuda:0") for _ in range(3))
-    out = torch.empty_like(q)
-    _warm(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.warmup)
+def _time(torch, fn, steps, warmup):
+    """Mean ms per call of fn(i) over `steps` calls after warmup, HIP events on
+    torch's current stream (the stream every launcher here is given)."""
+    _warm(torch, fn, warmup)
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
     e0.record(st)
-    for _ in range(args.steps):
-        ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd")
+    for i in range(steps):
+        fn(i)
     e1.record(st)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
+    return e0.elapsed_time(e1) / steps
+
+
+def _headline_inputs(torch):
+    """configs[1] inputs, N(0,1) bf16 drawn on the CPU from seed 42 (the CPU
+    baseline runs on the same bits)."""
+    B, S, H = 2, 8192, 24
+    g = torch.Generator().manual_seed(42)
+    return tuple(torch.randn(B, S, H, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+
+
+def bench_attention(args, torch, ma, _lib, qkv_cpu):
+    B, S, H = 2, 8192, 24
+    mode = args.mode
+    q, k, v = (t.to("cuda:0") for t in qkv_cpu)
+    out = torch.empty_like(q)
     flops = attention_flops(B, H, S, S)
+    t0 = time.perf_counter()
+    ms = _time(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.steps,
+               args.warmup)
+    wall = time.perf_counter() - t0
 
     # Dominant kernel alone: forward kernel over a pre-transposed V_t, events on
     # the launch stream (torch's current stream, passed to the C ABI).
@@ -79,17 +96,10 @@ def bench_attention(args, torch, ma, _lib):
     rc = getattr(_lib.lib, f"launch_v_transpose_{mode}")(_lib.ptr(v), _lib.ptr(vt), B * H * S, S, H, 1, sp)
     assert rc == 0, rc
     fwd = getattr(_lib.lib, f"launch_attention_forward_{mode}")
-    reps = max(args.steps, 5)
-    for _ in range(2):
-        fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S, 128, 1, None, sp)
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record(st)
-    for _ in range(reps):
-        rc = fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S, 128, 1, None, sp)
-    k1.record(st)
-    torch.cuda.synchronize()
-    assert rc == 0, rc
-    kms = k0.elapsed_time(k1) / reps
+    rcs = []
+    kms = _time(torch, lambda i: rcs.append(fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S,
+                                                128, 1, None, sp)), max(args.steps, 5), 2)
+    assert set(rcs) == {0}, set(rcs)
     achieved = flops / (kms * 1e-3) / 1e12
     traffic = None
     tfile = ROOT / "profiles" / "attn_fwd_traffic.json"
@@ -111,11 +121,79 @@ def bench_attention(args, torch, ma, _lib):
     }
 
 
-def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
+# The reference's published MI300X times (README.md:98-121), other hardware:
+# context for the extra legs, not a baseline of this metric.
+REF_MI300X_MS = {
+    ("headline", "rtne"): 3.083, ("headline", "rtna"): 3.022, ("headline", "rtz"): 2.983,
+    ("1x32x16384", "rtne"): 8.013, ("2x8x86016", "rtne"): 101.071,
+}
+
+
+def _leg(name, B, H, Sq, Skv, ms, **extra):
+    tf = attention_flops(B, H, Sq, Skv) / (ms * 1e-3) / 1e12
+    rec = {"shape_bshd": [B, Sq, H, 128], "skv": Skv, "ms": round(ms, 4), "tflops": round(tf, 1),
+           "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+    rec.update(extra)
+    _log(f"bench: attention {name}: {ms:.3f} ms, {tf:.0f} TFLOP/s")
+    return rec
+
+
+def bench_attention_extra(args, torch, ma, qkv_cpu):
+    """Other round modes, the reference benchmark's input pattern, the long
+    configs and the tail KV-split (one `forward` call per step, as the headline)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import realistic_bf16
+
+    res = {}
+    q, k, v = (t.to("cuda:0") for t in qkv_cpu)
+    out = torch.empty_like(q)
+    for mode in ("rtne", "rtna", "rtz"):
+        ms = _time(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.steps,
+                   args.warmup)
+        res[f"headline_{mode}"] = _leg(f"headline {mode}", 2, 24, 8192, 8192, ms, round_mode=mode,
+                                       ref_mi300x_ms=REF_MI300X_MS[("headline", mode)])
+    qr, kr, vr = (t.to("cuda:0") for t in realistic_bf16(2, 8192, 24, seed=42))
+    ms = _time(torch, lambda i: ma.forward(qr, kr, vr, out=out, round_mode="rtne", layout="bshd"), args.steps,
+               args.warmup)
+    res["headline_realistic_rtne"] = _leg("headline realistic rtne", 2, 24, 8192, 8192, ms, round_mode="rtne",
+                                          inputs="log-normal K row norms (reference benchmark/runner.py:34-47)")
+    del q, k, v, qr, kr, vr, out
+    g = torch.Generator(device="cuda:0")
+    for B, H, S, steps in ((1, 32, 16384, args.steps), (2, 8, 86016, max(3, args.steps // 6))):
+        g.manual_seed(61)
+        q, k, v = (torch.randn(B, S, H, 128, generator=g, device="cuda:0").to(torch.bfloat16) for _ in range(3))
+        o = torch.empty_like(q)
+        ms = _time(torch, lambda i: ma.forward(q, k, v, out=o, round_mode="rtne", layout="bshd"), steps, 2)
+        key = f"{B}x{H}x{S}"
+        res[f"long_{key}_rtne"] = _leg(f"long {key} rtne", B, H, S, S, ms, round_mode="rtne",
+                                       ref_mi300x_ms=REF_MI300X_MS[(key, "rtne")])
+        del q, k, v, o
+    # A shape whose last round of CTAs the tail planner splits: 17 q-blocks x 48
+    # heads = 816 CTAs = 3 rounds of 256 + a 48-CTA tail.
+    B, H, Sq, Skv = 2, 24, 4097, 8192
+    g.manual_seed(17)
+    q = torch.randn(B, Sq, H, 128, generator=g, device="cuda:0").to(torch.bfloat16)
+    k, v = (torch.randn(B, Skv, H, 128, generator=g, device="cuda:0").to(torch.bfloat16) for _ in range(2))
+    o = torch.empty_like(q)
+    for label, env in (("split", None), ("no_split", "1")):
+        if env:
+            os.environ["MOONMATH_NO_TAIL"] = env
+        try:
+            ms = _time(torch, lambda i: ma.forward(q, k, v, out=o, round_mode="rtne", layout="bshd"), args.steps,
+                       args.warmup)
+        finally:
+            os.environ.pop("MOONMATH_NO_TAIL", None)
+        res[f"tail_{label}_2x24_sq4097_skv8192_rtne"] = _leg(f"tail {label}", B, H, Sq, Skv, ms, round_mode="rtne")
+    return res
+
+
+def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1)), cpu=True):
     """B=64 absorbed-MLA paged decode, ctx ~ U[1024, 8192], 64-token
     pages over a randomly permuted pool, OCP e4m3fn KV, scale 1/sqrt(192).
     Three independent (Q, pool, table) sets rotate so the ~640 MB working set
-    exceeds the 256 MB Infinity Cache: each timed call streams its KV from HBM."""
+    exceeds the 256 MB Infinity Cache: each timed call streams its KV from HBM.
+    With ``cpu``, each config also times the reference test's fp32 formula over
+    the same 64 requests on the host (median of 3)."""
     sys.path.insert(0, str(ROOT / "tests"))
     from mla_inputs import KV_SCALE, SCALE_192, paged_pool, ragged_lens, rand_q
 
@@ -124,15 +202,17 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
     sum_l = sum(lens)
     n_blocks = sum(-(-l // 64) for l in lens)
     results = []
-    sets = []
+    sets, cpu_sets = [], []
     for r in range(3):
         pool, idx, indptr = paged_pool(lens, 100 + r)
+        cpu_sets.append((pool, idx, indptr))
         sets.append((pool.to("cuda:0"), idx.to("cuda:0"), indptr.to("cuda:0")))
     lens_t = torch.tensor(lens, dtype=torch.int32, device="cuda:0")
     for H, q_len in configs:
-        qs = []
+        qs, qs_cpu = [], []
         for r in range(3):
             q_lat, q_pe = rand_q(B, q_len, H, 200 + r, peak=1.0)
+            qs_cpu.append((q_lat, q_pe))
             o = torch.empty(B, q_len, H, 512, dtype=torch.bfloat16, device="cuda:0")
             qs.append((q_lat.to("cuda:0"), q_pe.to("cuda:0"), o))
         parts = ma.mla_decode_a16w8_plan_parts_q(B, 8192, q_len, H)
@@ -145,27 +225,22 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
                 ma.mla_decode_a16w8_paged_dev(q_lat[:, 0], q_pe[:, 0], pool, o[:, 0], lens_t, None, idx, indptr,
                                               parts, SCALE_192, KV_SCALE)
 
-        _warm(torch, call, warmup)
-        st = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for r in range(steps):
-            call(r)
-        e1.record(st)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / steps
+        us = _time(torch, call, steps, warmup) * 1e3
         # Algorithmic bytes: KV once + Q in + O out + block tables and lengths.
         nbytes = sum_l * 576 + B * q_len * H * (576 + 512) * 2 + 4 * (n_blocks + B)
         flops = 2.0 * (576 + 512) * H * q_len * sum_l
         gbs = nbytes / (us * 1e-6) / 1e9
         tfs = flops / (us * 1e-6) / 1e12
-        results.append({
+        rec = {
             "B": B, "H": H, "q_len": q_len, "parts": parts, "us": round(us, 2),
             "hbm_GBs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
             "mfma_TFLOPs": round(tfs, 1), "pct_bf16_peak": round(100 * tfs / PEAK_BF16_TFLOPS, 2),
             "bytes": nbytes,
-        })
+        }
         _log(f"bench: mla H={H} q_len={q_len}: {us:.1f} us, {gbs:.0f} GB/s, {tfs:.0f} TFLOP/s")
+        if cpu:
+            rec["cpu_baseline"] = mla_cpu_baseline(torch, qs_cpu[0], cpu_sets[0], lens, nbytes, flops)
+        results.append(rec)
     return {
         "metric": "MLA decode HBM GB/s (% peak)",
         "workload": "B=64 ctx~U[1024,8192] (seed 5) 64-token pages, fp8 e4m3fn KV, 3 rotating pools",
@@ -174,30 +249,79 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1))):
     }
 
 
-def cpu_baseline(torch, budget_s):
-    """The reference's CPU oracle formula, fp32 torch on this host, one head at a
-    time of the headline shape (S=8192), until ~budget_s seconds have elapsed."""
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(cores)
+def _cpu_threads():
+    """Host threads for the CPU baselines: every core of this process's
+    affinity, within the CPU share the GPU box gives one GPU's jobs
+    (OMP_NUM_THREADS there)."""
+    aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(aff, share) if share > 0 else aff), aff
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median3(fn):
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[1]
+
+
+def mla_cpu_baseline(torch, q_cpu, set_cpu, lens, nbytes, flops):
+    """The reference test's fp32 decode formula (tests/test_mla_decode.py:50-66)
+    with OCP e4m3fn dequant, over all 64 requests of one (Q, pool) set."""
+    from oracle.mla import torch_formula_cpu
+    from mla_inputs import KV_SCALE, SCALE_192
+
+    threads, aff = _cpu_threads()
+    torch.set_num_threads(threads)
+    q_lat, q_pe = q_cpu
+    pool, idx, indptr = set_cpu
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    t = _median3(lambda: torch_formula_cpu(q_lat, q_pe, pool, lens_t, idx, indptr, SCALE_192, KV_SCALE))
+    return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "tflops": round(flops / t / 1e12, 4),
+            "ms": round(t * 1e3, 1), "cores": threads, "kind": "port",
+            "sample": "all 64 requests, one (Q, pool) set, median of 3 runs"}
+
+
+def cpu_baseline(torch, qkv_cpu):
+    """The reference's CPU oracle formula (examples/basic.py:16-17), fp32 torch on
+    this host, over the whole headline workload (48 (b, h) heads, one at a time
+    to bound memory), on the same input bits as the GPU run; median of 3 runs."""
+    threads, aff = _cpu_threads()
+    torch.set_num_threads(threads)
     from oracle.attention import torch_formula_cpu
 
-    g = torch.Generator().manual_seed(42)
-    S = 8192
-    done, t_total = 0, 0.0
-    while t_total < budget_s and done < 480:
-        q, k, v = (torch.randn(1, 1, S, 128, generator=g).to(torch.bfloat16) for _ in range(3))
-        t0 = time.perf_counter()
-        torch_formula_cpu(q, k, v)
-        t_total += time.perf_counter() - t0
-        done += 1
-    flops = attention_flops(1, done, S, S)
+    q, k, v = qkv_cpu
+    B, S, H, _ = q.shape
+
+    def run():
+        for b in range(B):
+            for h in range(H):
+                torch_formula_cpu(q[b:b + 1, :, h].unsqueeze(1), k[b:b + 1, :, h].unsqueeze(1),
+                                  v[b:b + 1, :, h].unsqueeze(1))
+
+    t = _median3(run)
+    flops = attention_flops(B, H, S, S)
     return {
-        "value": round(flops / t_total / 1e12, 4),
+        "value": round(flops / t / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
-        "sample": f"{done} heads (each one (b,h) slice) of the (2,24,8192,128) headline shape, fp32 torch "
-                  f"softmax(q@k^T/sqrt(128))@v per head, {t_total:.1f} s",
+        "cpu_model": _cpu_model(),
+        "sample": f"the whole (2,24,8192,128) headline workload, fp32 torch softmax(q@k^T/sqrt(128))@v one (b,h) "
+                  f"head at a time, median of 3 runs ({t:.2f} s each); {threads} threads "
+                  f"(this process's affinity: {aff} cores)",
     }
 
 
@@ -207,9 +331,9 @@ def main():
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--mode", default="rtne", choices=["rtne", "rtna", "rtz"])
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the extra attention legs")
     ap.add_argument("--only", choices=["attention", "mla", "copy"], default=None,
                     help="run one leg only (for rocprofv3 counter passes); 'copy' runs a plain "
                          "1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE")
@@ -235,22 +359,24 @@ def main():
         _log(f"bench: copied {n} bytes x3 (calibration)")
         return
     if args.only == "mla":
-        print(json.dumps(bench_mla(torch, ma, args.steps, args.warmup)), flush=True)
+        print(json.dumps(bench_mla(torch, ma, args.steps, args.warmup, cpu=False)), flush=True)
         return
     _log("bench: attention headline (2,8192,24,128) bshd")
-    att = bench_attention(args, torch, ma, _lib)
+    qkv_cpu = _headline_inputs(torch)
+    att = bench_attention(args, torch, ma, _lib, qkv_cpu)
     _log(f"bench: attention {att['value']:.1f} TFLOP/s, kernel {att['kernel_ms']:.3f} ms")
     if args.only == "attention":
         print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"]}), flush=True)
         return
+    extra = None if args.no_extra else bench_attention_extra(args, torch, ma, qkv_cpu)
     mla = None
     if not args.no_mla:
         _log("bench: mla decode")
-        mla = bench_mla(torch, ma, args.steps, args.warmup)
+        mla = bench_mla(torch, ma, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
     cpu = None
     if not args.no_cpu_baseline:
         _log("bench: cpu baseline")
-        cpu = cpu_baseline(torch, args.cpu_budget)
+        cpu = cpu_baseline(torch, qkv_cpu)
     line = {
         "metric": "attn fwd TFLOP/s (% bf16 MFMA peak); MLA decode HBM GB/s (% peak)",
         "value": round(att["value"], 2),
@@ -272,6 +398,8 @@ def main():
         "roofline": att["roofline"],
         "cpu_baseline": cpu,
     }
+    if extra is not None:
+        line["attention"] = extra
     if mla is not None:
         line["mla"] = mla
     print(json.dumps(line), flush=True)

@@ -117,6 +117,31 @@ def fp32_reference(q_lat, q_pe, kv_u8, seq_lens, scale, kv_scale, kv_indices=Non
     return out
 
 
+def torch_formula_cpu(q_lat, q_pe, pool, seq_lens, kv_indices, kv_indptr, scale, kv_scale):
+    """The reference test's fp32 loop (tests/test_mla_decode.py:50-66) in CPU
+    torch over a paged pool: per request, gather its rows by kv_indices,
+    dequantise (OCP e4m3fn -> fp32, * kv_scale), then per draft position t
+    softmax((q_lat . k_lat + q_pe . k_pe) * scale) @ k_lat over the end-aligned
+    window. q_lat [B,q_len,H,512], q_pe [B,q_len,H,64] bf16; pool [slots,1,576]
+    float8_e4m3fn; seq_lens / kv_indices / kv_indptr int32. Returns fp32
+    [B,q_len,H,512]. (The CPU baseline the bench times.)"""
+    import torch
+
+    B, q_len, H, _ = q_lat.shape
+    flat = pool.view(-1, QK)
+    out = torch.empty(B, q_len, H, LAT, dtype=torch.float32)
+    for b in range(B):
+        S = int(seq_lens[b])
+        start = int(kv_indptr[b])
+        k = flat.index_select(0, kv_indices[start:start + S].long()).float() * kv_scale
+        k_lat, k_pe = k[:, :LAT], k[:, LAT:]
+        for t in range(q_len):
+            end = S - q_len + t + 1
+            score = (q_lat[b, t].float() @ k_lat[:end].T + q_pe[b, t].float() @ k_pe[:end].T) * scale
+            out[b, t] = torch.softmax(score, dim=-1) @ k_lat[:end]
+    return out
+
+
 def smoke_check(ma, torch):
     """Tiny paged MLA decode on cuda:0 vs the oracle (used by __graft_entry__.smoke)."""
     g = torch.Generator().manual_seed(11)

@@ -2,7 +2,7 @@
 csrc/attention_kernel.hip:1349-1393 (mirror: tools/tail_speedup.py:33-73) with
 the CU count re-derived for MI355X.
 
-``slots`` = CUs x CTAs resident per CU (256 x 2 for this build's 128-row CTAs).
+``slots`` = CUs x CTAs resident per CU (256 x 1 for this build's 256-row CTAs).
 No split when the grid tiles the slots evenly, when the last round is > 95%
 full, or when there are fewer than 48 kv blocks. Otherwise G minimises
 ceil(tail*G/slots) * ceil(nkb/G) + 3 over G <= max_parts/tail with

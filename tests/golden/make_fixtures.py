@@ -32,7 +32,7 @@ def attention_fixture():
     v = torch.randn(1, 2, 150, 128, generator=g).to(torch.bfloat16)
     out = {"q": bits(q), "k": bits(k), "v": bits(v)}
     for mode in ("rtne", "rtna", "rtz"):
-        o, _, a = oa.forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), mode, aux=True)
+        o, _, a, _ = oa.forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), mode, aux=True)
         out[f"out_{mode}"] = o
         out[f"scale_{mode}"] = a.astype(np.float16)  # tolerance floor only; half precision suffices
     np.savez_compressed(HERE / "attention_bhsd_1x2x80x150.npz", **out)

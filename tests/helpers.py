@@ -1,4 +1,7 @@
 """Shared test helpers: seeded inputs and the bf16 tolerance rule."""
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -6,22 +9,28 @@ from oracle import bf16 as ob
 
 # Tolerance rule for the attention forward (bf16 out, fp32 accumulate), all
 # three must hold on every compared tensor:
-#  1. |got - ref| <= 1 bf16 ULP of max(|ref|, FLOOR_REL * A), where ref is the
-#     oracle's bf16 output under the same round mode and
-#     A = sum_j P_j |v_jd| / sum_j p_j is the element's absolute scale.
+#  1. |got - ref| <= ulp_bf16(max(|ref|, FLOOR_REL * A)) + T, where ref is the
+#     oracle's bf16 output under the same round mode,
+#     A = sum_j P_j |v_jd| / sum_j p_j is the element's absolute scale and T
+#     the oracle's near-tie allowance (sum over terms whose fp32 p_j lies
+#     within the GPU's fp32 error of a bf16 rounding boundary of
+#     ulp_bf16(P_j) |v_jd| / sum_j p_j).
 #     Why a floor: the kernel's fp32 scores and v_exp_f32 differ from the
 #     oracle's in the last fp32 bit, which flips the bf16 rounding of a P term
 #     now and then (about 4e-4 of terms). One flip moves the element by up to
 #     2^-7 * P_j |v_jd| / l -- far below one ULP of A, but unbounded in ULPs of
 #     an element that cancels to near zero. FLOOR_REL = 1/4 covers a flip of
-#     any term that carries <= 1/8 of the absolute mass.
+#     any term that carries <= 1/8 of the absolute mass; T covers a flip of a
+#     term that carries more (peaked attention: growing keys, spikes, the
+#     reference benchmark's log-normal key norms), which moves the element by
+#     up to 1 ULP before the output rounding.
 #  2. >= MIN_EXACT of the elements are bit-identical to the oracle;
 #  3. >= MIN_STRICT of the elements are within 1 ULP of |ref| itself (no floor).
 # 2 and 3 catch systematic deviations (a wrong P rounding mode, a biased
 # rescale) that stay under rule 1.
 FLOOR_REL = 0.25
-MIN_EXACT = 0.98
-MIN_STRICT = 0.995
+MIN_EXACT = 0.99
+MIN_STRICT = 0.999
 
 
 def randn_bf16(shape, seed, scale=1.0):
@@ -30,6 +39,41 @@ def randn_bf16(shape, seed, scale=1.0):
     if scale != 1.0:
         x = x * scale
     return x.to(torch.bfloat16)
+
+
+def realistic_bf16(B, S, H, seed, D=128, sigma=0.6):
+    """The reference benchmark's "realistic" pattern (reference
+    benchmark/runner.py:34-47), BSHD: Q, V ~ N(0, 1); K = uniform direction with
+    magnitude exp(N(0, sigma)) * sqrt(D) (log-normal row norms). Drawn on the
+    CPU from a seeded generator (the reference draws on the GPU from seed 42)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, H, D, generator=g)
+    k_dir = torch.randn(B, S, H, D, generator=g)
+    k_dir = k_dir / k_dir.norm(dim=-1, keepdim=True)
+    log_norm = torch.randn(B, S, H, 1, generator=g) * sigma
+    k = k_dir * (torch.exp(log_norm) * D ** 0.5)
+    v = torch.randn(B, S, H, D, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def growth_log2(q_head, k_head, block=64):
+    """Per row: integer-grid max over all keys minus the one over the first
+    block (log2 units) -- how far a row's max grows past its first block."""
+    from oracle import attention as oa
+
+    s_all = (q_head.astype(np.float64) @ k_head.astype(np.float64).T).astype(np.float32)
+    return oa.row_max_int(s_all) - oa.row_max_int(s_all[:, :block])
+
+
+def log_stats(name, stats):
+    """Append one parity record to $MOONMATH_PARITY_LOG (a JSON-lines file);
+    name None = the running pytest case."""
+    path = os.environ.get("MOONMATH_PARITY_LOG")
+    if path:
+        if name is None:
+            name = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0].split("::")[-1]
+        with open(path, "a") as f:
+            f.write(json.dumps({"case": name, **stats}) + "\n")
 
 
 def bits(t):
@@ -45,9 +89,19 @@ def to_bhsd(a, layout):
     return a.transpose(0, 2, 1, 3) if layout == "bshd" else a
 
 
-def compare_bf16(got, ref, scale=None, floor_rel=FLOOR_REL):
-    """got/ref: uint16 bit arrays (same shape). Returns stats dict; asserts
-    NaN positions/bits, Inf identity and the ULP rule."""
+def check_fractions(stats, min_exact=MIN_EXACT, min_strict=MIN_STRICT):
+    """Rules 2 and 3 on a stats dict (statistical: applied to >= 1000 elements,
+    over all the tensors of one case when they are compared piecewise)."""
+    if stats["n"] >= 1000:
+        assert stats["exact"] >= min_exact, f"too few bit-exact elements: {stats}"
+        assert stats["strict_le1"] >= min_strict, f"too many elements beyond strict 1 ULP: {stats}"
+
+
+def compare_bf16(got, ref, scale=None, tie=None, floor_rel=FLOOR_REL, min_exact=MIN_EXACT,
+                 min_strict=MIN_STRICT, fractions=True):
+    """got/ref: uint16 bit arrays (same shape); scale = A, tie = T from the
+    oracle. Returns stats dict; asserts NaN positions/bits, Inf identity and
+    the ULP rule, and (``fractions``) rules 2 and 3."""
     g = ob.bf16_to_f32(got).astype(np.float64)
     r = ob.bf16_to_f32(ref).astype(np.float64)
     gn, rn = np.isnan(g), np.isnan(r)
@@ -68,13 +122,15 @@ def compare_bf16(got, ref, scale=None, floor_rel=FLOOR_REL):
     if scale is not None:
         mag = np.maximum(np.abs(r[fin]), floor_rel * scale[fin])
         u = ob.ulp_bf16(mag)
+        if tie is not None:
+            stats["n_tie"] = int((d > u).sum())  # elements within the rule only through T
+            u = u + tie[fin]
         ratio = d / u
         stats["rule_max"] = float(ratio.max()) if d.size else 0.0
         bad = ratio > 1.0
         assert not bad.any(), (
             f"{int(bad.sum())} elements beyond 1 ULP (rule), worst {stats['rule_max']:.2f}; stats={stats}"
         )
-    if d.size >= 1000:
-        assert stats["exact"] >= MIN_EXACT, f"too few bit-exact elements: {stats}"
-        assert stats["strict_le1"] >= MIN_STRICT, f"too many elements beyond strict 1 ULP: {stats}"
+    if fractions:
+        check_fractions(stats, min_exact, min_strict)
     return stats

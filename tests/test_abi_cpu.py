@@ -36,9 +36,11 @@ def test_library_exports_header_symbol(name):
 
 
 def test_attention_geometry():
+    """One 8-wave CTA of 256 q rows per CU, 64-row kv blocks, 256 CUs, 1024
+    split parts (the workspace size follows from these)."""
     geo = _lib.geometry()
-    assert geo["kv_block"] == 64 and geo["rows_per_cta"] in (128, 256)
-    assert geo["slots"] in (256, 512)
+    assert geo == {"rows_per_cta": 256, "kv_block": 64, "slots": 256, "max_parts": 1024}
+    assert _lib.lib.tail_workspace_bytes_rtne() == 1024 * 256 * (128 + 2) * 4
 
 
 @pytest.mark.parametrize("B,H,S,Skv", [(2, 24, 8192, 8192), (2, 24, 4097, 512), (2, 8, 86016, 86016),
@@ -50,6 +52,13 @@ def test_tail_planner_matches_oracle(B, H, S, Skv):
     nkb = -(-Skv // 64)
     want = planner.plan_tail(nqb, B * H, nkb, geo["slots"], geo["max_parts"])
     assert _lib.plan_tail(B, H, S, Skv) == want
+
+
+def test_tail_planner_splits_the_4097_shape():
+    """(2,24,4097,8192): 17 q-blocks x 48 heads = 816 CTAs, a 48-CTA tail over
+    128 kv blocks. G = 16: 768 parts in 3 rounds of 8 blocks, 3 * 8 + 3 = 27,
+    beats G = 5 (240 parts, one round of 26 blocks: 29) and no split (131)."""
+    assert _lib.plan_tail(2, 24, 4097, 8192) == (768, 48, 16, 768)
 
 
 def test_tail_planner_disabled_and_forced():

@@ -108,7 +108,7 @@ def _rand(shape, seed, scale=1.0):
 
 def test_attention_matches_fp64_softmax_without_p_rounding():
     q, k, v = _rand((1, 2, 70, 128), 1), _rand((1, 2, 150, 128), 2), _rand((1, 2, 150, 128), 3)
-    _, pre, _ = oa.forward(q, k, v, ob.RTNE, p_round=False, aux=True)
+    _, pre, _, _ = oa.forward(q, k, v, ob.RTNE, p_round=False, aux=True)
     s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)) / math.sqrt(128)
     s -= s.max(-1, keepdims=True)
     p = np.exp(s)
@@ -119,8 +119,8 @@ def test_attention_matches_fp64_softmax_without_p_rounding():
 def test_attention_p_rounding_effect_is_bounded():
     """With P rounded the result moves by at most 2^-8 relative of the absolute scale."""
     q, k, v = _rand((1, 1, 64, 128), 4), _rand((1, 1, 300, 128), 5), _rand((1, 1, 300, 128), 6)
-    _, pre, scl = oa.forward(q, k, v, ob.RTZ, aux=True)
-    _, pre_u, _ = oa.forward(q, k, v, ob.RTZ, p_round=False, aux=True)
+    _, pre, scl, _ = oa.forward(q, k, v, ob.RTZ, aux=True)
+    _, pre_u, _, _ = oa.forward(q, k, v, ob.RTZ, p_round=False, aux=True)
     assert np.all(np.abs(pre - pre_u) <= 2.0 ** -7 * scl)
     assert np.any(pre != pre_u)  # rounding is actually applied
 
@@ -134,7 +134,7 @@ def test_attention_hand_case():
     v = np.zeros((1, 1, 2, 128), np.float32)
     v[0, 0, 0, 0], v[0, 0, 1, 0] = 1.0, 2.0
     k[0, 0, 1, 0] = np.float32(1.0 / c)  # s1 * c ~= 1
-    out, pre, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
+    out, pre, _, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
     x1 = np.float32(np.float64(np.float32(1.0 / c)) * c)
     m = np.ceil(x1)
     p0, p1 = 2.0 ** (0 - m), 2.0 ** (np.float64(x1) - m)
@@ -192,7 +192,7 @@ def test_nan_inf_semantics():
     k[0, 0, :, :] = -np.inf * np.sign(q[0, 0, 0])[None, :]  # all scores of row 0 -> -inf
     k[0, 0, :, 1:] = 0
     k[0, 0, :, 0] = -np.inf if q[0, 0, 0, 0] > 0 else np.inf
-    out, pre, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
+    out, pre, _, _ = oa.forward(q, k, v, ob.RTNE, aux=True)
     row0 = ob.bf16_to_f32(out[0, 0, 0])
     assert np.all(row0 == 0.0)  # l == 0 -> output 0 (reference :1114-1117)
 
@@ -266,12 +266,12 @@ def test_tolerance_rule_rejects_wrong_p_rounding(out_mode, p_mode):
     from helpers import compare_bf16
 
     q, k, v = _rand((1, 1, 64, 128), 30), _rand((1, 1, 1024, 128), 31), _rand((1, 1, 1024, 128), 32)
-    ref, _, scl = oa.forward(q, k, v, out_mode, aux=True)
+    ref, _, scl, tie = oa.forward(q, k, v, out_mode, aux=True)
     bad = oa.forward(q, k, v, out_mode, p_mode=p_mode)
     with pytest.raises(AssertionError):
-        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0])
+        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0], tie[0, 0])
     good = oa.head_forward_blocked(q[0, 0], k[0, 0], v[0, 0], out_mode, kv_block=64, split_ways=3)
-    compare_bf16(good, ref[0, 0], scl[0, 0])
+    compare_bf16(good, ref[0, 0], scl[0, 0], tie[0, 0])
 
 
 def _plant(kind, q, k, v, mode):
@@ -292,7 +292,108 @@ def test_tolerance_rule_rejects_planted_mistakes(kind):
     from helpers import compare_bf16
 
     q, k, v = _rand((1, 1, 64, 128), 40), _rand((1, 1, 300, 128), 41), _rand((1, 1, 300, 128), 42)
-    ref, _, scl = oa.forward(q, k, v, ob.RTNE, aux=True)
+    ref, _, scl, tie = oa.forward(q, k, v, ob.RTNE, aux=True)
     bad = _plant(kind, q, k, v, ob.RTNE)
     with pytest.raises(AssertionError):
-        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0])
+        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0], tie[0, 0])
+
+
+def test_forward_rows_equals_full_forward_rows():
+    q, k, v = _rand((1, 3, 90, 128), 4), _rand((1, 3, 200, 128), 5), _rand((1, 3, 200, 128), 6)
+    full, _, scl, _ = oa.forward(q, k, v, ob.RTNA, aux=True)
+    rows = np.array([0, 7, 63, 64, 89])
+    part, _, pscl, _ = oa.forward_rows(q, k, v, ob.RTNA, "bhsd", [(0, 2), (0, 0)], rows, aux=True)
+    assert np.array_equal(part[0], full[0, 2, rows]) and np.array_equal(part[1], full[0, 0, rows])
+    assert np.allclose(pscl[0], scl[0, 2, rows])
+
+
+def test_nan_rows_rule_matches_full_oracle():
+    """The short-cut NaN-row rule against the full computation: +inf keys give
+    a row-dependent mix (sign of q at the inf dimension), a NaN key poisons all."""
+    q, k, v = _rand((1, 1, 120, 128), 7), _rand((1, 1, 90, 128), 8), _rand((1, 1, 90, 128), 9)
+    k_inf = k.copy()
+    k_inf[0, 0, 3, 10] = np.inf
+    k_inf[0, 0, 50, 99] = -np.inf
+    rows = oa.nan_rows(q[0, 0], k_inf[0, 0])
+    full = oa.forward(q, k_inf, v, ob.RTNE)[0, 0]
+    got_nan = (full & 0x7FFF) > 0x7F80
+    assert rows.any() and not rows.all()
+    assert np.array_equal(got_nan, np.broadcast_to(rows[:, None], got_nan.shape))
+    k_nan = k.copy()
+    k_nan[0, 0, 70, 1] = np.nan
+    assert oa.nan_rows(q[0, 0], k_nan[0, 0]).all()
+    assert not oa.nan_rows(q[0, 0], k[0, 0]).any()
+
+
+def _kernel_model(Q, K, V, mode, block=64, grow=2.0 ** 20):
+    """An fp32 model of the GPU kernel's numerics, independent of the oracle's
+    fp64 path: scores accumulated in fp32 over 8 steps of 16 dims (one MFMA
+    each), the integer max fixed at the first block and raised (exact power of
+    two rescale of O and l) only for rows of a block whose p exceed ``grow``,
+    O and l accumulated in fp32 block by block."""
+    c = np.float64(oa.SCALE_LOG2E)
+    Sq, Skv = Q.shape[0], K.shape[0]
+    Q64, K64, V64 = Q.astype(np.float64), K.astype(np.float64), V.astype(np.float64)
+    s = np.zeros((Sq, Skv), np.float32)
+    for ds in range(8):
+        part = Q64[:, 16 * ds:16 * ds + 16] @ K64[:, 16 * ds:16 * ds + 16].T
+        s = (s.astype(np.float64) + part).astype(np.float32)
+    m = None
+    O = np.zeros((Sq, 128), np.float32)
+    l = np.zeros(Sq, np.float32)
+    for r0 in range(0, Skv, block):
+        sb = s[:, r0:r0 + block]
+        bm = oa.row_max_int(sb)
+        m = bm if m is None else m
+        p = oa.softmax_p(sb, m)
+        up = (p > grow).any(axis=1)
+        if up.any():
+            m_new = np.where(up, np.maximum(m, bm), m)
+            sc = np.exp2((m - m_new).astype(np.float64)).astype(np.float32)
+            O *= sc[:, None]
+            l *= sc
+            m = m_new.astype(np.float32)
+            p = oa.softmax_p(sb, m)
+        P = ob.round_f32(p, mode).astype(np.float64)
+        O = (O.astype(np.float64) + (P @ V64[r0:r0 + block]).astype(np.float32)).astype(np.float32)
+        l = (l.astype(np.float64) + p.astype(np.float64).sum(axis=1).astype(np.float32)).astype(np.float32)
+    inv = np.where(l == 0, np.float32(0), (1.0 / np.where(l == 0, 1, l)).astype(np.float32))
+    return ob.round_bits((O * inv[:, None]).astype(np.float32), mode, canon=True)
+
+
+def _rising(seed, Sq=256, Skv=2048, top_log2=4.0):
+    q, k, v = _rand((1, 1, Sq, 128), seed), _rand((1, 1, Skv, 128), seed + 1), _rand((1, 1, Skv, 128), seed + 2)
+    k = (k * np.exp2(np.arange(Skv) * (top_log2 / Skv))[None, None, :, None]).astype(np.float32)
+    k = torch.from_numpy(k).to(torch.bfloat16).float().numpy()
+    return q, k, v
+
+
+@pytest.mark.parametrize("mode", [ob.RTNE, ob.RTNA, ob.RTZ])
+@pytest.mark.parametrize("seed", [50, 53])
+def test_tolerance_rule_accepts_fp32_kernel_model_on_peaked_inputs(mode, seed):
+    """Peaked attention (key norms rising 16x along the sequence, every row's
+    max raised several times): the fp32 kernel model passes the rule, and the
+    near-tie allowance T stays targeted -- above a tenth of the element's ULP
+    only where a near-tie P term carries real weight (a few percent of the
+    elements at most)."""
+    from helpers import compare_bf16
+
+    q, k, v = _rising(seed)
+    ref, _, scl, tie = oa.forward(q, k, v, mode, aux=True)
+    got = _kernel_model(q[0, 0], k[0, 0], v[0, 0], mode)
+    stats = compare_bf16(got, ref[0, 0], scl[0, 0], tie[0, 0])
+    assert stats["exact"] < 1.0  # the model is a different computation, not the oracle
+    r = ob.bf16_to_f32(ref[0, 0]).astype(np.float64)
+    u = ob.ulp_bf16(np.maximum(np.abs(r), 0.25 * scl[0, 0]))
+    assert float((tie[0, 0] > 0.1 * u).mean()) < 0.03
+
+
+@pytest.mark.parametrize("out_mode,p_mode", [(ob.RTNE, ob.RTZ), (ob.RTZ, ob.RTNE)])
+def test_tolerance_rule_rejects_wrong_p_rounding_on_peaked_inputs(out_mode, p_mode):
+    from helpers import compare_bf16
+
+    q, k, v = _rising(56)
+    ref, _, scl, tie = oa.forward(q, k, v, out_mode, aux=True)
+    bad = oa.forward(q, k, v, out_mode, p_mode=p_mode)
+    with pytest.raises(AssertionError):
+        compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0], tie[0, 0])

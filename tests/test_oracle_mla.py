@@ -94,3 +94,18 @@ def test_rows_remap():
     rev = om.decode(ql[::-1].copy(), qp[::-1].copy(), fp8_bits(pool), lens, SCALE_576, KV_SCALE,
                     kv_indices=idx.numpy(), kv_indptr=indptr.numpy(), rows=rows)
     assert np.array_equal(rev[::-1], base)
+
+
+def test_torch_formula_cpu_matches_numpy_fp32_reference():
+    """The bench's CPU baseline (torch, paged gather) against the numpy fp32
+    formula of the reference test (tests/test_mla_decode.py:50-66)."""
+    from mla_inputs import paged_pool, rand_q
+
+    lens = [70, 129, 64]
+    pool, idx, indptr = paged_pool(lens, 9)
+    q_lat, q_pe = rand_q(3, 2, 4, 9)
+    got = om.torch_formula_cpu(q_lat, q_pe, pool, torch.tensor(lens, dtype=torch.int32), idx, indptr,
+                               SCALE_576, KV_SCALE).numpy()
+    ref = om.fp32_reference(q_lat.float().numpy(), q_pe.float().numpy(), pool.view(torch.uint8).numpy(), lens,
+                            SCALE_576, KV_SCALE, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-5)
