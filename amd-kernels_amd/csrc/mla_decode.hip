@@ -47,6 +47,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "mla_common.hpp"
@@ -814,6 +815,40 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   return e == hipSuccess ? 0 : (int)e;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free launches: the split records and merge table of one launch
+// live in a file-scope device array (64.3 MiB, zero-filled at load, held on
+// every GPU the library runs on until the process ends). Its device address
+// is looked up once per device with hipGetSymbolAddress and kept; host code
+// never hands the array's name itself to a kernel (on the host that name is a
+// stand-in, not a device address). The decode writes every record and table
+// entry the merge reads, so nothing needs clearing between calls; calls that
+// overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchRecords = 32768;  // B * parts * H * q_len at most
+constexpr size_t kScratchBytes = kScratchRecords * (kLat + 2) * sizeof(float) + (size_t)kMaxPagedB * 8;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (0 or a HIP error code).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return -10;
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!ptr) {
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return -10;
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -847,6 +882,25 @@ int launch_mla_decode_a16w8_paged_dev(const void* q_lat, const void* q_pe, const
   (void)kv_bytes;
   return launch(q_lat, q_pe, kv_pool, o_lat, seq_lens, rows, kv_indices, kv_indptr, B, H, 0, parts, q_len, lat_dim,
                 rope_dim, scale, kv_scale, workspace, stream, true);
+}
+
+int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_pe, const void* kv_pool, void* o_lat,
+                                              const void* seq_lens, const void* rows, const void* kv_indices,
+                                              const void* kv_indptr, int B, int H, int parts, int lat_dim,
+                                              int rope_dim, float scale, float kv_scale, float scale_p, void* stream,
+                                              size_t kv_bytes, int q_len) {
+  (void)scale_p;
+  (void)kv_bytes;
+  if (B < 1 || B > kMaxPagedB || H < 1 || H > kMaxHeads || q_len < 1 || q_len > kMaxQLen) return -4;
+  const int eff = clamp_parts(parts, B, H, q_len, true);
+  void* ws = nullptr;
+  if (eff > 1) {
+    if ((size_t)B * eff * H * q_len > kScratchRecords) return -9;
+    const int rc = scratch_ptr(&ws);
+    if (rc != 0) return rc;
+  }
+  return launch(q_lat, q_pe, kv_pool, o_lat, seq_lens, rows, kv_indices, kv_indptr, B, H, 0, eff, q_len, lat_dim,
+                rope_dim, scale, kv_scale, ws, stream, true);
 }
 
 int launch_mla_decode_a16w8_multiq(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, int B, int H,

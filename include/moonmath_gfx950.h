@@ -78,7 +78,9 @@ size_t moonmath_attention_vt_bytes(int batch, int heads, int seq_len_kv);
  * Absorbed-MLA decode: bf16 q_lat [.., 512] / q_pe [.., 64], fused fp8 OCP
  * e4m3fn KV rows of 576 bytes, per-tensor kv_scale, bf16 o_lat written in
  * place. H in [1,128], q_len in [1,8]. Codes: -2 lat/rope dims, -3 H,
- * -4 q_len or B, -6 null pointer, -7 S < 1, -8 grid overflow.
+ * -4 q_len or B, -6 null pointer, -7 S < 1, -8 grid overflow, -9 split
+ * records beyond the allocation-free entry point's array, -10 no device
+ * address for that array.
  * ------------------------------------------------------------------------- */
 
 /* Fixed split-workspace cap in bytes. Replaces csrc/mla_decode_a16w8.hip:178-181. */
@@ -103,6 +105,22 @@ int launch_mla_decode_a16w8_paged_dev(const void* q_lat, const void* q_pe, const
                                       const void* kv_indptr, int B, int H, int parts, int lat_dim, int rope_dim,
                                       float scale, float kv_scale, float scale_p, void* workspace, void* stream,
                                       size_t kv_bytes, int q_len);
+
+/* Allocation-free variant of launch_mla_decode_a16w8_paged_dev (same arguments
+ * and results, q_len 1..8, no workspace argument). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). The split records
+ * live in a 64.3 MiB device array of the library (held on each GPU the library
+ * runs on until the process ends); the call performs no allocation. Limit:
+ * B * parts * H * q_len <= 32768 split records once parts is clamped as in
+ * the workspace launcher (parts 1 needs none), else returns -9 with nothing
+ * launched. Calls that overlap on one GPU share the array and race: serialise
+ * them (one stream, or events). */
+int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_pe, const void* kv_pool, void* o_lat,
+                                              const void* seq_lens, const void* rows, const void* kv_indices,
+                                              const void* kv_indptr, int B, int H, int parts, int lat_dim,
+                                              int rope_dim, float scale, float kv_scale, float scale_p, void* stream,
+                                              size_t kv_bytes, int q_len);
 
 /* Multi-query (draft window) contiguous decode. Replaces
  * csrc/mla_decode_a16w8_multiq.hip:955-983. */
