@@ -27,6 +27,11 @@
 //    (the "tail") can be split over KV into G contiguous block ranges; each
 //    part writes unnormalised fp32 (O, m, l) and a merge kernel combines them
 //    (reference :1094-1112, :1239-1279).
+//  * LiteAttention (reference :629-716, :1296-1347, :1497-1542, :1599-1681):
+//    the same kernel walks only the KV blocks its CTA's read list (an int16
+//    run-length row) names, votes per block whether any of its rows came
+//    within `threshold` (log2) of the row's running max, and writes the next
+//    step's list; a planning kernel orders the CTAs heaviest first (LPT).
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -62,6 +67,15 @@ constexpr int kMaxParts = 1024;
 constexpr size_t kPartOFloats = (size_t)kMaxRows * kD;
 constexpr size_t kWorkspaceBytes = (size_t)kMaxParts * kMaxRows * (kD + 2) * sizeof(float);
 
+// LiteAttention: a CTA's processed block list (int16 ids, bit 15 marks the
+// last block of a read-list range) and per-block vote bytes follow the rings.
+constexpr int kMaxLiteBlocks = 8192;  // kv blocks per head (Skv <= 524288)
+constexpr int kLiteListOff = kLdsBytes;
+constexpr int kLiteVoteOff = kLiteListOff + kMaxLiteBlocks * 2;
+constexpr int kLiteMiscOff = kLiteVoteOff + kMaxLiteBlocks;
+constexpr int kLdsLiteBytes = kLiteMiscOff + 64;
+static_assert(kLdsLiteBytes <= 160 * 1024, "lite LDS fits a CU");
+
 struct Params {
   const uint16_t* q;
   const uint16_t* k;
@@ -74,11 +88,87 @@ struct Params {
   int prefix_wgs;    // CTAs that run the whole KV stream
   int split_ways;    // G (parts per tail q-block)
   float scale_log2e; // log2(e) / sqrt(128), rounded to fp32 on the host
+  // LiteAttention only.
+  const int16_t* read_list;   // [B*H][nqb][nkb + 2]
+  int16_t* write_list;        // same shape
+  const int16_t* must_do;     // [len, s0, e0, ...] or null
+  const int* order;           // LPT permutation of the CTAs, or null
+  float threshold;            // log2 units, < 0
+  int phase;                  // 1: ranges ascend, 0: descend
 };
 
 // Element offset of (b, h, s=0, d=0) and the stride between seq positions.
 __device__ __forceinline__ long long head_base(int b, int h, int S, int H, int bshd) {
   return bshd ? ((long long)b * S * H + h) * kD : ((long long)b * H + h) * (long long)S * kD;
+}
+
+// ---------------------------------------------------------------------------
+// LiteAttention write list of one CTA, by wave 0 after the main loop: the
+// run-length row of the next step (reference record(), :685-716), in the
+// processing order of this step. Block i is skipped iff no wave voted to keep
+// it and no must_do range [s, e) holds it. A marker (the block id) is written
+// at every change of the skip state, which starts as "skip" at the first
+// block and again after the last block of each read-list range; after a kept
+// range-end block the marker block + lstep closes its range. Lanes take one
+// block each and place their 0..2 markers by a prefix sum over the wave.
+// Markers past the row's nkb + 1 slots are dropped (possible only for read
+// rows no writer produces) and the count keeps whole pairs.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_excl_sum(int x, int lane) {
+  int incl = x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += y;
+  }
+  return incl - x;
+}
+
+__device__ __forceinline__ void lite_emit(const Params& p, long long row, int n, int lstep, const int16_t* list,
+                                          uint8_t* vote, int lane) {
+  int16_t* out = p.write_list + row;
+  int md_len = p.must_do ? (int)p.must_do[0] : 0;
+  md_len = md_len < 0 ? 0 : md_len;
+  // Pass 1: vote byte -> skip flag (1 = skip).
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    if (i < n) {
+      const int blk = list[i] & 0x7FFF;
+      bool keep = vote[i] != 0;
+      for (int m = 1; m + 1 <= md_len && !keep; m += 2) keep = blk >= p.must_do[m] && blk < p.must_do[m + 1];
+      vote[i] = keep ? 0 : 1;
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // Pass 2: markers.
+  const int cap = p.nkb + 1;
+  int base = 0;
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    int blk = 0, cntm = 0;
+    bool skip = true, rend = false, flip = false;
+    if (i < n) {
+      const int e = list[i];
+      blk = e & 0x7FFF;
+      rend = (e & 0x8000) != 0 || i == n - 1;
+      skip = vote[i] != 0;
+      const bool before = (i == 0 || (list[i - 1] & 0x8000) != 0) ? true : (vote[i - 1] != 0);
+      flip = skip != before;
+      cntm = (int)flip + (int)(rend && !skip);
+    }
+    const int ex = wave_excl_sum(cntm, lane);
+    int pos = 1 + base + ex;
+    if (flip) {
+      if (pos <= cap) out[pos] = (int16_t)blk;
+      ++pos;
+    }
+    if (rend && !skip && pos <= cap) out[pos] = (int16_t)(blk + lstep);
+    base += __shfl(ex + cntm, 63, 64);
+  }
+  if (lane == 0) {
+    const int len = base <= cap ? base : (cap & ~1);
+    out[0] = (int16_t)len;
+  }
 }
 
 // One CTA = 8 waves (two per SIMD) = 256 q rows of one (b, h), one CTA per CU,
@@ -100,7 +190,7 @@ __device__ __forceinline__ long long head_base(int b, int h, int S, int H, int b
 // bf16(P) under the final max times an exact power of two (up to the last
 // fp32 bit of the exp2 argument): the output does not depend on where the
 // rebases happen, on the KV blocking or on the split.
-template <int MODE>
+template <int MODE, bool LITE>
 __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb_begin, int kb_end, int part,
                                          char* lds) {
   const int tid = threadIdx.x;
@@ -170,6 +260,69 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     for (int ds = 0; ds < 8; ++ds) qf[ds] = *reinterpret_cast<const bf16x8*>(src + ds * 16);
   }
 
+  // ---- the processed block sequence ---------------------------------------------
+  // Dense: kb_begin .. kb_end-1. Lite: the blocks the CTA's read-list row names,
+  // decoded into LDS in processing order (reference cursor :629-668): ranges are
+  // taken from the end of the row; range (s, e) yields s+d, s+2d, ... while
+  // strictly before e+d, at least one block (d = +1 in phase 1, -1 in phase 0).
+  // Ids outside [0, nkb) are dropped and the list is capped at kMaxLiteBlocks,
+  // so no row content makes the kernel read or write out of bounds.
+  int16_t* lite_list = reinterpret_cast<int16_t*>(lds + kLiteListOff);
+  uint8_t* lite_vote = reinterpret_cast<uint8_t*>(lds + kLiteVoteOff);
+  int* lite_misc = reinterpret_cast<int*>(lds + kLiteMiscOff);
+  const long long lite_row = ((long long)bh * p.nqb + qb) * (p.nkb + 2);
+  const int lstep = p.phase ? 1 : -1;
+  int nblk = kb_end - kb_begin;
+  if constexpr (LITE) {
+    // Stage the row (nkb + 2 int16) in the K ring, then wave 0 expands it.
+    int16_t* stage = reinterpret_cast<int16_t*>(lds);
+    const int row_len = p.nkb + 2;
+    for (int e = tid; e < row_len; e += kThreads) stage[e] = p.read_list[lite_row + e];
+    for (int e = tid; e < kMaxLiteBlocks / 4; e += kThreads) reinterpret_cast<uint32_t*>(lite_vote)[e] = 0u;
+    lds_reads_done_barrier();
+    if (wave == 0) {
+      int len = stage[0];
+      len = len < 0 ? 0 : (len > p.nkb + 1 ? p.nkb + 1 : len);
+      int n = 0;
+      for (int idx = len; idx >= 2 && n < kMaxLiteBlocks; idx -= 2) {
+        const int start = stage[idx] + lstep;
+        const int stop = stage[idx - 1] + lstep;
+        const int span = (stop - start) * lstep;
+        const int cnt = span > 1 ? span : 1;  // blocks start + j * lstep, j < cnt
+        // j range whose block lies in [0, nkb)
+        int jlo, jhi;
+        if (lstep > 0) {
+          jlo = start < 0 ? -start : 0;
+          jhi = p.nkb - start;
+        } else {
+          jlo = start >= p.nkb ? start - p.nkb + 1 : 0;
+          jhi = start + 1;
+        }
+        jhi = jhi < cnt ? jhi : cnt;
+        if (jhi - jlo > kMaxLiteBlocks - n) jhi = jlo + (kMaxLiteBlocks - n);
+        if (jhi <= jlo) continue;
+        for (int j0 = jlo; j0 < jhi; j0 += 64) {
+          const int j = j0 + lane;
+          if (j < jhi) {
+            const int blk = start + j * lstep;
+            lite_list[n + (j - jlo)] = (int16_t)(blk | (j == jhi - 1 ? 0x8000 : 0));
+          }
+        }
+        n += jhi - jlo;
+      }
+      if (lane == 0) lite_misc[0] = n;
+    }
+    lds_reads_done_barrier();
+    nblk = __builtin_amdgcn_readfirstlane(lite_misc[0]);
+  }
+  auto blk_of = [&](int i) -> int {
+    if constexpr (LITE) {
+      return __builtin_amdgcn_readfirstlane(lite_list[i] & 0x7FFF);
+    } else {
+      return kb_begin + i;
+    }
+  };
+
   auto qk = [&](const char* kst, f32x16 (&s)[2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) s[t] = f32x16{};
@@ -210,9 +363,13 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   };
   float row_m = kNegFltMax, row_l = 0.f;
 
+  // Lite vote state: each row's exact running max of s*c (log2 units) over the
+  // blocks processed so far (reference softmax_update's row_max, :398-436).
+  float run_mx = -__builtin_inff();
+  const bool row_valid = q_row0 + r < p.Sq;
+
   f32x16 sA[2], sB[2];
   bf16x8 pf[2][2];
-  const int nblk = kb_end - kb_begin;
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
@@ -221,9 +378,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       issue_k(kb, slot);
       issue_v(kb, slot);
     };
-    issue_kv(kb_begin, 0);
-    if (nblk > 1) issue_kv(kb_begin + 1, 1);
-    if (nblk > 2) issue_kv(kb_begin + 2, 2);
+    issue_kv(blk_of(0), 0);
+    if (nblk > 1) issue_kv(blk_of(1), 1);
+    if (nblk > 2) issue_kv(blk_of(2), 2);
     // 4 DMAs per wave per block: block 0 has landed, blocks 1 and 2 stay in flight.
     if (nblk > 2) {
       wait_vmem_barrier<8>();
@@ -233,11 +390,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       wait_vmem_barrier<0>();
     }
     qk(kring, sA);
-    mask(sA, kb_begin);
+    mask(sA, blk_of(0));
     row_m = fmaxf(block_max(sA, 0), kNegFltMax);
 
-    auto step = [&](int kb, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
-      const int i = kb - kb_begin;
+    auto step = [&](int i, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
+      const int kb = blk_of(i);
       // Block i+1 has landed (block i+2 stays in flight, 4 DMAs per wave); every
       // wave is done with step i-1, so the slot of block i-1 is free.
       sched_fence();
@@ -251,11 +408,12 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // 8 waves issuing theirs back to back after the barrier stall their QK);
       // a partial last block is gathered here.
       const bool dma3 = i + 3 < nblk;
-      const bool dma3_full = dma3 && (kb + 4) * kKvBlock <= p.Skv;
-      if (dma3 && !dma3_full) issue_kv(kb + 3, (i + 3) % kRing);
+      const int kb3 = dma3 ? blk_of(i + 3) : kb;
+      const bool dma3_full = dma3 && (kb3 + 1) * kKvBlock <= p.Skv;
+      if (dma3 && !dma3_full) issue_kv(kb3, (i + 3) % kRing);
       const int pd3 = __builtin_amdgcn_readfirstlane((int)dma3_full);
-      const char* kbase3 = kh + (long long)(kb + 3) * kblk_bytes;
-      const char* vbase3 = vth + (long long)(kb + 3) * kVBytes;
+      const char* kbase3 = kh + (long long)kb3 * kblk_bytes;
+      const char* vbase3 = vth + (long long)kb3 * kVBytes;
       const char* kst3 = kring + ((i + 3) % kRing) * kKBytes;
       const char* vst3 = vring + ((i + 3) % kRing) * kVBytes;
       auto dma3_step = [&](int d) {  // d = 0, 1: K instructions; 2, 3: V instructions
@@ -362,6 +520,22 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       pack_pf(0);
       __builtin_amdgcn_s_setprio(0);
+      if constexpr (LITE) {
+        // Keep the block for the next step if some valid row's block max came
+        // within `threshold` of its running max (reference :983-995); the
+        // first processed block is always kept.
+        float bm = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) bm = fmaxf(bm, scur[t][e]);
+        bm = xor32_max(bm) * c;
+        const bool keep = row_valid && (bm - run_mx > p.threshold);
+        run_mx = fmaxf(run_mx, bm);
+        if ((__builtin_amdgcn_ballot_w64(keep) != 0 || i == 0) && lane == 0)
+          __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(lite_vote) + (i >> 2), (1u << wave) << ((i & 3) * 8),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       // Wave-uniform growth tests: row tile 0 and the first half of row tile 1
       // before any PV of this block, the second half of row tile 1 before its PV.
       if (__builtin_amdgcn_ballot_w64(fmaxf(lpart[0] + lpart[1], lpart[2]) > kGrowLimit) != 0) {
@@ -391,13 +565,17 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
     };
-    for (int kb = kb_begin; kb < kb_end; kb += 2) {
-      step(kb, sA, sB);
-      if (kb + 1 < kb_end) step(kb + 1, sB, sA);
+    for (int i = 0; i < nblk; i += 2) {
+      step(i, sA, sB);
+      if (i + 1 < nblk) step(i + 1, sB, sA);
     }
   }
   sched_fence();
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  if constexpr (LITE) {
+    lds_reads_done_barrier();  // every wave's votes are in
+    if (wave == 0) lite_emit(p, lite_row, nblk, lstep, lite_list, lite_vote, lane);
+  }
 
   // ---- epilogue -----------------------------------------------------------------
   row_l = xor32_sum(row_l);
@@ -444,7 +622,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
   const int idx = blockIdx.x;
   if (idx < p.prefix_wgs) {
     const int w = xcd_remap(idx, p.prefix_wgs);
-    run_tile<MODE>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
+    run_tile<MODE, false>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
   } else {
     // Split part: tail q-block t, part j of G, contiguous kv-block range.
     const int part = idx - p.prefix_wgs;
@@ -452,7 +630,83 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
     const int w = p.prefix_wgs + t;
     const int kb0 = (int)((long long)p.nkb * j / p.split_ways);
     const int kb1 = (int)((long long)p.nkb * (j + 1) / p.split_ways);
-    run_tile<MODE>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
+    run_tile<MODE, false>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
+  }
+}
+
+// LiteAttention forward: one CTA per (b, h, q-block); grid slot i runs CTA
+// order[i] (LPT order) or, without an order, the XCD-grouped dense mapping.
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void attn_lite_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsLiteBytes];
+  const int total = p.nqb * p.B * p.H;
+  const int w = p.order ? p.order[blockIdx.x] : xcd_remap(blockIdx.x, total);
+  if (w < 0 || w >= total) return;
+  run_tile<MODE, true>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
+}
+
+// ---------------------------------------------------------------------------
+// LPT order of the lite CTAs (reference plan_lite_order, :1296-1347): CTAs
+// sorted by the number of blocks their read-list row keeps, heaviest first, in
+// 64 buckets of kept/(nkb+1); a stable counting sort (thread t owns the
+// contiguous CTA range [t*C, (t+1)*C)), so the order is deterministic. One
+// CTA of 256 threads; up to kLptMaxCtas CTAs.
+// ---------------------------------------------------------------------------
+constexpr int kLptThreads = 256;
+constexpr int kLptBuckets = 64;
+constexpr int kLptMaxCtas = 65536;
+
+__device__ __forceinline__ int lite_kept(const int16_t* row, int nkb) {
+  int len = row[0];
+  len = len < 0 ? 0 : (len > nkb + 1 ? nkb + 1 : len);
+  int kept = 0;
+  for (int i = len; i >= 2; i -= 2) {
+    const int d = (int)row[i] - (int)row[i - 1];
+    kept += d < 0 ? -d : d;
+  }
+  return kept;
+}
+
+__global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const int16_t* __restrict__ read_list,
+                                                                int* __restrict__ order, int nctas, int nkb) {
+  __shared__ int hist[kLptBuckets][kLptThreads];
+  __shared__ int bucket_base[kLptBuckets];
+  const int t = threadIdx.x;
+  const int chunk = (nctas + kLptThreads - 1) / kLptThreads;
+  const int w0 = t * chunk;
+  const int w1 = w0 + chunk < nctas ? w0 + chunk : nctas;
+  for (int b = 0; b < kLptBuckets; ++b) hist[b][t] = 0;
+  auto bucket = [&](int w) {
+    const int kept = lite_kept(read_list + (long long)w * (nkb + 2), nkb);
+    const int bk = kept * kLptBuckets / (nkb + 1);
+    return bk < kLptBuckets ? bk : kLptBuckets - 1;
+  };
+  for (int w = w0; w < w1; ++w) ++hist[bucket(w)][t];
+  __syncthreads();
+  // Exclusive prefix over (bucket descending, thread ascending).
+  if (t < kLptBuckets) {
+    int sum = 0;
+    for (int u = 0; u < kLptThreads; ++u) {
+      const int c = hist[t][u];
+      hist[t][u] = sum;
+      sum += c;
+    }
+    bucket_base[t] = sum;  // bucket total, turned into a base below
+  }
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int b = kLptBuckets - 1; b >= 0; --b) {
+      const int c = bucket_base[b];
+      bucket_base[b] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  for (int w = w0; w < w1; ++w) {
+    const int bk = bucket(w);
+    order[bucket_base[bk] + hist[bk][t]] = w;
+    ++hist[bk][t];
   }
 }
 
@@ -654,6 +908,55 @@ int launch_fwd(const void* q, const void* k, const void* v_t, void* out, int bat
   return e == hipSuccess ? 0 : (int)e;
 }
 
+// LiteAttention launcher (reference launch_attention_forward_lite,
+// attention_kernel.hip:1599-1681). workspace: lite_workspace_bytes ints for
+// the LPT order (null = plain order); LPT runs when the kv range is long
+// enough to amortise its planning launch (48 blocks, as the reference).
+constexpr int kLiteMinKvBlocksForLpt = 48;
+
+template <int MODE>
+int launch_lite(const void* q, const void* k, const void* v_t, void* out, int batch, int heads, int seq_len,
+                int seq_len_kv, int head_dim, const void* read_list, void* write_list, const void* must_do,
+                float threshold, int phase, int layout, void* workspace, void* stream) {
+  if (batch <= 0 || heads <= 0) return 1;
+  if (seq_len <= 0) return 2;
+  if (head_dim != kD) return 3;
+  if (!read_list || !write_list) return 4;
+  if (seq_len_kv <= 0) return 5;
+  if (layout != 0 && layout != 1) return 7;
+  if (!q || !k || !v_t || !out) return 8;
+  Params p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.vt = static_cast<const uint16_t*>(v_t);
+  p.out = static_cast<uint16_t*>(out);
+  p.B = batch;
+  p.H = heads;
+  p.Sq = seq_len;
+  p.Skv = seq_len_kv;
+  p.bshd = layout;
+  p.nqb = (seq_len + kRowsPerCta - 1) / kRowsPerCta;
+  p.nkb = (seq_len_kv + kKvBlock - 1) / kKvBlock;
+  if (p.nkb > kMaxLiteBlocks) return 6;
+  p.scale_log2e = (float)(1.4426950408889634 / 11.313708498984761);
+  p.read_list = static_cast<const int16_t*>(read_list);
+  p.write_list = static_cast<int16_t*>(write_list);
+  p.must_do = static_cast<const int16_t*>(must_do);
+  p.threshold = threshold;
+  p.phase = phase ? 1 : 0;
+  const long long total = (long long)p.nqb * batch * heads;
+  if (total > 0x7FFFFFFFLL) return 9;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (workspace && p.nkb >= kLiteMinKvBlocksForLpt && total <= kLptMaxCtas) {
+    p.order = static_cast<const int*>(workspace);
+    hipLaunchKernelGGL(lite_order_kernel, dim3(1), dim3(kLptThreads), 0, st, p.read_list,
+                       static_cast<int*>(workspace), (int)total, p.nkb);
+  }
+  hipLaunchKernelGGL((attn_lite_kernel<MODE>), dim3((unsigned)total), dim3(kThreads), 0, st, p);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
+}
+
 int launch_vt(const void* v, void* v_t, int n_rows, int seq_len_per_head, int heads, int layout, void* stream) {
   if (heads <= 0 || seq_len_per_head <= 0 || n_rows <= 0) return 1;
   if (n_rows % ((long long)heads * seq_len_per_head) != 0) return 2;
@@ -685,7 +988,19 @@ extern "C" {
     return launch_fwd<MODE>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, layout, workspace, \
                             0, stream);                                                                      \
   }                                                                                                          \
-  size_t tail_workspace_bytes_##NAME(void) { return kWorkspaceBytes; }
+  size_t tail_workspace_bytes_##NAME(void) { return kWorkspaceBytes; }                                     \
+  int launch_attention_forward_lite_##NAME(const void* q, const void* k, const void* v_t, void* out, int batch, \
+                                           int heads, int seq_len, int seq_len_kv, int head_dim,              \
+                                           const void* read_list, void* write_list, const void* must_do_list, \
+                                           float threshold, int phase, int layout, void* workspace,           \
+                                           void* stream) {                                                    \
+    return launch_lite<MODE>(q, k, v_t, out, batch, heads, seq_len, seq_len_kv, head_dim, read_list,          \
+                             write_list, must_do_list, threshold, phase, layout, workspace, stream);          \
+  }                                                                                                          \
+  size_t lite_workspace_bytes_##NAME(int batch, int heads, int seq_len) {                                    \
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;                                                  \
+    return (size_t)batch * heads * ((seq_len + kRowsPerCta - 1) / kRowsPerCta) * sizeof(int);                \
+  }
 
 MM_ATTN_MODE_SYMBOLS(rtne, mm::kRTNE)
 MM_ATTN_MODE_SYMBOLS(rtna, mm::kRTNA)

@@ -10,6 +10,7 @@ kernels in ``libmoonmath_gfx950.so`` called through ctypes.
 """
 
 from ._kernel import forward, forward_lite
+from .lite import LiteAttention
 from .mla import (
     mla_decode_a16w8,
     mla_decode_a16w8_multiq,
@@ -22,7 +23,7 @@ from .mla import (
 )
 
 __all__ = [
-    "forward", "forward_lite",
+    "forward", "forward_lite", "LiteAttention",
     "mla_decode_a16w8", "mla_decode_a16w8_paged_dev",
     "mla_decode_a16w8_plan_parts", "mla_decode_a16w8_plan_parts_capped",
     "mla_decode_a16w8_plan_parts_q",

@@ -146,9 +146,86 @@ def _forward_device(q, k, v, out, round_mode, layout):
     return out
 
 
-def forward_lite(*args, **kwargs):
-    """LiteAttention skip-list forward (reference moonmath_attention/_kernel.py:85-134).
+def _check_list(t, name, q, min_numel):
+    # reference csrc/attention_api.cpp:322-336; the size check is this build's
+    # (the kernel reads and writes whole rows of [B,H,qtiles,ktiles+2]).
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be torch.Tensor; got {type(t).__name__}")
+    if t.dtype != torch.int16:
+        raise ValueError(f"{name} must be int16, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device != q.device:
+        raise ValueError(f"{name} must be on the same device as q")
+    if t.numel() < min_numel:
+        raise ValueError(f"{name} must hold at least {min_numel} int16 ([B,H,qtiles,ktiles+2]), got {t.numel()}")
 
-    Not part of this build: the hot path here is the dense forward.
+
+def forward_lite(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    read_list: torch.Tensor,
+    write_list: torch.Tensor,
+    *,
+    threshold: float,
+    phase: int,
+    must_do_list: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    round_mode: str = "rtna",
+    layout: str = "bhsd",
+) -> torch.Tensor:
+    """LiteAttention forward: only the K-blocks the skip list names are computed.
+
+    Mirrors reference moonmath_attention/_kernel.py:85-134 and
+    csrc/attention_api.cpp:283-440 (GPU tensors only). ``read_list`` /
+    ``write_list`` are int16 [B, H, qtiles, ktiles+2] run-length rows (qtiles =
+    ceil(Sq/256), ktiles = ceil(Skv/64)): ``read_list`` names the blocks this
+    step computes, the kernel writes the next step's list into ``write_list``
+    (a block is kept when some q row of the tile came within ``threshold``
+    (log2, < 0) of its running max; the first processed block always). ``phase``
+    1 walks ranges ascending, 0 descending. ``must_do_list`` (int16
+    [len, s0, e0, ...], end exclusive) pins processed blocks as kept.
+    MOONMATH_LITE_PLAIN=1 disables the LPT (heaviest-first) CTA order.
+    With a compute-all read list the output is attention over every key.
     """
-    raise NotImplementedError("forward_lite (LiteAttention skip lists) is not implemented in the gfx950 build")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be torch.Tensor; got {type(t).__name__}")
+    B, H, Sq, Skv, lay = check_args(q, k, v, out, round_mode, layout)
+    nqb = -(-Sq // 256)
+    nkb = -(-Skv // 64)
+    need = B * H * nqb * (nkb + 2)
+    _check_list(read_list, "read_list", q, need)
+    _check_list(write_list, "write_list", q, need)
+    if must_do_list is not None:
+        _check_list(must_do_list, "must_do_list", q, 1)
+        # The kernel reads must_do_list[0] entries after the first: they must
+        # exist (one host sync, only when a list is given).
+        n_md = int(must_do_list[0].item())
+        if n_md < 0 or n_md > must_do_list.numel() - 1:
+            raise ValueError(f"must_do_list[0] = {n_md} but the list holds {must_do_list.numel() - 1} entries after it")
+    if out is None:
+        out = torch.empty_like(q)
+    dev = q.device
+    lib = _lib.lib
+    with torch.cuda.device(dev):
+        stream = _lib.stream_ptr(dev)
+        vt = torch.empty(lib.moonmath_attention_vt_bytes(B, H, Skv) // 2, dtype=torch.bfloat16, device=dev)
+        ws = None
+        if os.environ.get("MOONMATH_LITE_PLAIN") is None:
+            ws = torch.empty(getattr(lib, f"lite_workspace_bytes_{round_mode}")(B, H, Sq), dtype=torch.uint8,
+                             device=dev)
+        rc = getattr(lib, f"launch_v_transpose_{round_mode}")(
+            _lib.ptr(v), _lib.ptr(vt), B * H * Skv, Skv, H, lay, stream
+        )
+        if rc != 0:
+            raise RuntimeError(f"launch_v_transpose returned error code {rc}")
+        rc = getattr(lib, f"launch_attention_forward_lite_{round_mode}")(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, Sq, Skv, 128,
+            _lib.ptr(read_list), _lib.ptr(write_list), _lib.ptr(must_do_list), float(threshold), int(phase), lay,
+            _lib.ptr(ws), stream,
+        )
+        if rc != 0:
+            raise RuntimeError(f"launch_attention_forward_lite returned error code {rc}")
+    return out

@@ -24,6 +24,9 @@ for _m in ("rtne", "rtna", "rtz"):
     SIGNATURES[f"launch_v_transpose_{_m}"] = (_i, [_p, _p, _i, _i, _i, _i, _p])
     SIGNATURES[f"launch_attention_forward_{_m}"] = (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p])
     SIGNATURES[f"tail_workspace_bytes_{_m}"] = (_sz, [])
+    SIGNATURES[f"launch_attention_forward_lite_{_m}"] = (
+        _i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _f, _i, _i, _p, _p])
+    SIGNATURES[f"lite_workspace_bytes_{_m}"] = (_sz, [_i, _i, _i])
 SIGNATURES.update({
     "moonmath_attention_forward_ex": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p, _i, _p]),
     "moonmath_attention_plan_tail": (_i, [_i, _i, _i, _i, _i, _i, _ip]),

@@ -187,6 +187,50 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
     return res
 
 
+def bench_lite(args, torch, ma, qkv_cpu):
+    """LiteAttention steps at the headline shape (RTNA, the class default):
+    the compute-all seed list, and read lists keeping the first block and a
+    seeded 25% of the others per 256-row tile (heaviest-first CTA order).
+    One step = one forward_lite call (V transpose + lite kernel + LPT plan)."""
+    import numpy as np
+
+    B, S, H = 2, 8192, 24
+    q, k, v = (t.to("cuda:0") for t in qkv_cpu)
+    out = torch.empty_like(q)
+    nqb, nkb = S // 256, S // 64
+    res = {}
+    rng = np.random.default_rng(9)
+    for label, frac in (("compute_all", 1.0), ("keep_25pct", 0.25)):
+        rows = np.zeros((B * H * nqb, nkb + 2), np.int16)
+        kept_total = 0
+        for i in range(len(rows)):
+            keep = np.concatenate([[True], rng.random(nkb - 1) < frac]) if frac < 1 else np.ones(nkb, bool)
+            # runs of kept blocks written as a phase-0 list, read ascending in phase 1
+            runs, b0 = [], None
+            for b in range(nkb):
+                if keep[b] and b0 is None:
+                    b0 = b
+                if (not keep[b] or b == nkb - 1) and b0 is not None:
+                    runs.append((b0, b if not keep[b] else nkb))
+                    b0 = None
+            vals = []
+            for lo, hi in reversed(runs):
+                vals += [hi - 1, lo - 1]
+            rows[i, 0] = len(vals)
+            rows[i, 1:1 + len(vals)] = vals
+            kept_total += int(keep.sum())
+        read = torch.from_numpy(rows).to("cuda:0")
+        write = torch.empty_like(read)
+        ms = _time(torch, lambda i: ma.forward_lite(q, k, v, read, write, threshold=-6.0, phase=1, out=out,
+                                                    round_mode="rtna", layout="bshd"), args.steps, args.warmup)
+        frac_kept = kept_total / (B * H * nqb * nkb)
+        eff = attention_flops(B, H, S, S) * frac_kept / (ms * 1e-3) / 1e12
+        res[label] = {"ms": round(ms, 4), "kept_fraction": round(frac_kept, 4),
+                      "tflops_on_kept_blocks": round(eff, 1)}
+        _log(f"bench: lite {label}: {ms:.3f} ms, kept {frac_kept:.3f}, {eff:.0f} TFLOP/s on kept blocks")
+    return res
+
+
 def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1)), cpu=True):
     """B=64 absorbed-MLA paged decode, ctx ~ U[1024, 8192], 64-token
     pages over a randomly permuted pool, OCP e4m3fn KV, scale 1/sqrt(192).
@@ -369,6 +413,7 @@ def main():
         print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"]}), flush=True)
         return
     extra = None if args.no_extra else bench_attention_extra(args, torch, ma, qkv_cpu)
+    lite = None if args.no_extra else bench_lite(args, torch, ma, qkv_cpu)
     mla = None
     if not args.no_mla:
         _log("bench: mla decode")
@@ -400,6 +445,8 @@ def main():
     }
     if extra is not None:
         line["attention"] = extra
+    if lite is not None:
+        line["lite"] = lite
     if mla is not None:
         line["mla"] = mla
     print(json.dumps(line), flush=True)

@@ -56,6 +56,37 @@ size_t tail_workspace_bytes_rtne(void);
 size_t tail_workspace_bytes_rtna(void);
 size_t tail_workspace_bytes_rtz(void);
 
+/* LiteAttention forward: only the K-blocks named by read_list (int16
+ * [B,H,ceil(Sq/256),ceil(Skv/64)+2] run-length rows: len, then (end, start)
+ * pairs read from the back, walked ascending when phase != 0, descending
+ * otherwise) are computed; write_list (same shape) receives the next step's
+ * rows: a processed block is kept when some q row of the 256-row tile came
+ * within `threshold` (log2) of its running max, when it is the first block
+ * processed, or when must_do_list (int16 [len, s0, e0, ...], end exclusive;
+ * nullable) holds it. v_t is the output of launch_v_transpose_<mode>.
+ * workspace: lite_workspace_bytes_<mode>() bytes for the heaviest-first CTA
+ * order, or NULL (plain order). Codes: as the dense launcher, plus 4 (NULL
+ * read or write list) and 6 (more than 8192 K-blocks, Skv > 524288).
+ * Replaces csrc/attention_api.cpp:67-104 / csrc/attention_kernel.hip:1604-1681. */
+int launch_attention_forward_lite_rtne(const void* q, const void* k, const void* v_t, void* out, int batch,
+                                       int heads, int seq_len, int seq_len_kv, int head_dim, const void* read_list,
+                                       void* write_list, const void* must_do_list, float threshold, int phase,
+                                       int layout, void* workspace, void* stream);
+int launch_attention_forward_lite_rtna(const void* q, const void* k, const void* v_t, void* out, int batch,
+                                       int heads, int seq_len, int seq_len_kv, int head_dim, const void* read_list,
+                                       void* write_list, const void* must_do_list, float threshold, int phase,
+                                       int layout, void* workspace, void* stream);
+int launch_attention_forward_lite_rtz(const void* q, const void* k, const void* v_t, void* out, int batch,
+                                      int heads, int seq_len, int seq_len_kv, int head_dim, const void* read_list,
+                                      void* write_list, const void* must_do_list, float threshold, int phase,
+                                      int layout, void* workspace, void* stream);
+
+/* Bytes of the lite CTA-order buffer (one int per 256-row q tile and head).
+ * Replaces csrc/attention_kernel.hip:1554-1558. */
+size_t lite_workspace_bytes_rtne(int batch, int heads, int seq_len);
+size_t lite_workspace_bytes_rtna(int batch, int heads, int seq_len);
+size_t lite_workspace_bytes_rtz(int batch, int heads, int seq_len);
+
 /* Mode-generic forward (round_mode 0 = RTNE, 1 = RTNA, 2 = RTZ). force_split_ways
  * > 1 forces that KV split on the last round of CTAs (test hook; 0 = planner).
  * Serves the Python wrapper that replaces csrc/attention_api.cpp:152-283. */

@@ -16,6 +16,9 @@ planner    tail KV-split planner (reference :1349-1393)
 fp8        OCP e4m3fn decode (OCP 8-bit floating point spec, v1.0)
 mla        absorbed-MLA paged decode (reference csrc/mla_decode_a16w8.hip:1-24,
            tests/test_mla_decode.py:50-66)
+lite       LiteAttention skip lists: read-row cursor, vote, write-row emitter,
+           LPT order (reference csrc/attention_kernel.hip:629-716, :983-995,
+           :1296-1347)
 
 Pinning: every function is checked in ``tests/test_oracle_*.py`` against
 hand-derived known answers, closed forms or library routines (torch's RTNE

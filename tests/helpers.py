@@ -97,6 +97,22 @@ def check_fractions(stats, min_exact=MIN_EXACT, min_strict=MIN_STRICT):
         assert stats["strict_le1"] >= min_strict, f"too many elements beyond strict 1 ULP: {stats}"
 
 
+def aggregate_stats(stats):
+    """Element-weighted totals of several compare_bf16 stats dicts."""
+    n = sum(s["n"] for s in stats)
+    agg = {
+        "n": n,
+        "exact": sum(s["exact"] * s["n"] for s in stats) / max(n, 1),
+        "strict_le1": sum(s["strict_le1"] * s["n"] for s in stats) / max(n, 1),
+        "strict_max": max(s["strict_max"] for s in stats),
+    }
+    if all("rule_max" in s for s in stats):
+        agg["rule_max"] = max(s["rule_max"] for s in stats)
+    if all("n_tie" in s for s in stats):
+        agg["n_tie"] = sum(s["n_tie"] for s in stats)
+    return agg
+
+
 def compare_bf16(got, ref, scale=None, tie=None, floor_rel=FLOOR_REL, min_exact=MIN_EXACT,
                  min_strict=MIN_STRICT, fractions=True):
     """got/ref: uint16 bit arrays (same shape); scale = A, tie = T from the

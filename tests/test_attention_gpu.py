@@ -19,8 +19,8 @@ import moonmath_attention as ma
 from moonmath_attention import _lib
 from oracle import attention as oa
 from oracle import vt_layout
-from helpers import (bits, check_fractions, compare_bf16, f32, growth_log2, log_stats, randn_bf16,
-                     realistic_bf16, to_bhsd)
+from helpers import (aggregate_stats, bits, check_fractions, compare_bf16, f32, growth_log2, log_stats,
+                     randn_bf16, realistic_bf16, to_bhsd)
 
 pytestmark = pytest.mark.gpu
 
@@ -69,19 +69,7 @@ def _check(q, k, v, out, mode, layout, heads, name, **bars):
     return agg
 
 
-def _aggregate(stats):
-    n = sum(s["n"] for s in stats)
-    agg = {
-        "n": n,
-        "exact": sum(s["exact"] * s["n"] for s in stats) / max(n, 1),
-        "strict_le1": sum(s["strict_le1"] * s["n"] for s in stats) / max(n, 1),
-        "strict_max": max(s["strict_max"] for s in stats),
-    }
-    if all("rule_max" in s for s in stats):
-        agg["rule_max"] = max(s["rule_max"] for s in stats)
-    if all("n_tie" in s for s in stats):
-        agg["n_tie"] = sum(s["n_tie"] for s in stats)
-    return agg
+_aggregate = aggregate_stats
 
 
 def _check_rows(q, k, v, out, mode, layout, heads, rows, name, **bars):

@@ -1,0 +1,210 @@
+"""GPU tests of LiteAttention (forward_lite + LiteAttention + LPT order).
+
+The reference's contracts (tests/test_attention.py:88-214), on this build's
+256-row tiles: the compute-all seed step equals the dense forward (here
+bit-identical, the reference checks against SDPA); the LPT order is
+bit-identical to the plain order; a must_do list pinning every block
+reproduces compute-all at every step; the learned list keeps exactly the hot
+blocks of each head. Beyond them: steps over non-trivial read lists in both
+phases against the oracle (output under the tolerance rule, written rows
+exactly), and the LPT permutation against the oracle's.
+"""
+import numpy as np
+import pytest
+import torch
+
+import moonmath_attention as ma
+from moonmath_attention import _lib
+from oracle import attention as oa
+from oracle import lite as ol
+from helpers import aggregate_stats, bits, check_fractions, compare_bf16, f32, log_stats, randn_bf16, to_bhsd
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+# Reference LITE_SHAPE (B=1, H=8, S=Skv=4096, D=128), 5 steps, threshold -3.
+B, H, S = 1, 8, 4096
+STEPS = 5
+THR = -3.0
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+
+
+def _uniform(layout):
+    q, k, v = (randn_bf16((B, S, H, 128), 7 + i) for i in range(3))
+    if layout == "bhsd":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    return q.to(DEV), k.to(DEV), v.to(DEV)
+
+
+def _peaked():
+    """Reference _lite_qkv_peaked: head h keeps K-blocks 0..h at scale 2, the
+    rest damped to 0.05, so the vote drops the cold blocks per head."""
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(B, S, H, 128, generator=g) for _ in range(3))
+    scale = torch.full((H, S), 0.05)
+    for h in range(H):
+        scale[h, : (h + 1) * 64] = 2.0
+    k = k * scale.t().view(1, S, H, 1)
+    return tuple(t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+
+
+def _run_lite(q, k, v, layout, steps, must_do=None):
+    attn = ma.LiteAttention(threshold=THR, round_mode="rtna", layout=layout)
+    out = None
+    for _ in range(steps):
+        out = attn(q, k, v, must_do_list=must_do)
+    torch.cuda.synchronize()
+    return out, attn
+
+
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+def test_lite_compute_all_equals_dense_forward(layout, monkeypatch):
+    """The seed step is the dense forward without the tail KV-split (which
+    lite never uses, as in the reference): bit-identical, and within the
+    tolerance rule of the oracle (2 sampled heads)."""
+    q, k, v = _uniform(layout)
+    attn = ma.LiteAttention(threshold=THR, round_mode="rtna", layout=layout)
+    lite = attn(q, k, v)
+    monkeypatch.setenv("MOONMATH_NO_TAIL", "1")
+    dense = ma.forward(q, k, v, round_mode="rtna", layout=layout)
+    torch.cuda.synchronize()
+    assert torch.equal(lite.view(torch.int16), dense.view(torch.int16))
+    got = to_bhsd(bits(lite), layout)
+    stats = []
+    for b, h in ((0, 0), (0, 5)):
+        ref, _, scl, tie = oa.forward(f32(q), f32(k), f32(v), "rtna", layout=layout, heads=[(b, h)], aux=True)
+        stats.append(compare_bf16(got[b, h], ref[b, h], scl[b, h], tie[b, h], fractions=False))
+    agg = aggregate_stats(stats)
+    log_stats(f"lite_compute_all_1x8x4096_{layout}_rtna", agg)
+    check_fractions(agg)
+
+
+def test_lite_lpt_matches_plain_bitexact(monkeypatch):
+    q, k, v = _peaked()
+    monkeypatch.delenv("MOONMATH_LITE_PLAIN", raising=False)
+    lpt, a1 = _run_lite(q, k, v, "bshd", STEPS)
+    monkeypatch.setenv("MOONMATH_LITE_PLAIN", "1")
+    plain, a2 = _run_lite(q, k, v, "bshd", STEPS)
+    assert torch.equal(lpt.view(torch.int16), plain.view(torch.int16)), "LPT order changed the output"
+    assert torch.equal(a1.read_list, a2.read_list)
+
+
+def test_lite_must_do_all_equals_compute_all():
+    q, k, v = _peaked()
+    ktiles = S // 64
+    must_do_all = torch.tensor([2, 0, ktiles], dtype=torch.int16, device=DEV)
+    ref = ma.LiteAttention(threshold=THR, round_mode="rtna", layout="bshd")(q, k, v)
+    forced, attn = _run_lite(q, k, v, "bshd", STEPS, must_do=must_do_all)
+    assert torch.equal(forced.view(torch.int16), ref.view(torch.int16))
+    kept = [ol.kept_count(attn.read_list[0, h, t].cpu().numpy(), ktiles) for h in range(H) for t in range(S // 256)]
+    assert kept == [ktiles] * len(kept)
+
+
+def test_lite_skip_list_develops():
+    q, k, v = _peaked()
+    ktiles = S // 64
+    attn = ma.LiteAttention(threshold=THR, round_mode="rtna", layout="bshd")
+    attn(q, k, v)
+    torch.cuda.synchronize()
+    assert ol.kept_count(attn.write_list[0, 0, 0].cpu().numpy(), ktiles) == ktiles  # the seed it read
+    assert ol.kept_count(attn.read_list[0, 0, 0].cpu().numpy(), ktiles) < ktiles
+    for _ in range(STEPS - 1):
+        attn(q, k, v)
+    torch.cuda.synchronize()
+    kept_by_head = [ol.kept_count(attn.read_list[0, h, 0].cpu().numpy(), ktiles) for h in range(H)]
+    assert kept_by_head == list(range(1, H + 1)), kept_by_head
+
+
+def _random_rows(nrows, nkb, phase, seed):
+    """Valid read rows as a writer in the other phase would produce them:
+    random kept subsets (first block of the previous walk always kept)."""
+    rng = np.random.default_rng(seed)
+    rows = np.zeros((nrows, nkb + 2), np.int16)
+    prev_phase = 1 - phase
+    for i in range(nrows):
+        blocks, ends = ol.decode(ol.seed_row(nkb), nkb, 1)
+        if prev_phase == 0:
+            blocks, ends = blocks[::-1], ends[::-1]
+            ends = [False] * (nkb - 1) + [True]
+        keep = [True] + [bool(x) for x in rng.random(nkb - 1) < rng.uniform(0.1, 0.9)]
+        row = ol.emit(blocks, ends, keep, prev_phase, nkb)
+        rows[i, :len(row)] = row
+    return rows
+
+
+@pytest.mark.parametrize("phase", [1, 0])
+@pytest.mark.parametrize("mode", ["rtna", "rtz"])
+def test_lite_step_matches_oracle(phase, mode):
+    """One step over random valid read rows (ragged Sq / Skv, BSHD): output of
+    sampled tiles under the tolerance rule, and every written row exactly."""
+    Bq, Hq, Sq, Skv = 2, 3, 700, 1500
+    nqb, nkb = -(-Sq // 256), -(-Skv // 64)
+    q, k, v = (randn_bf16((Bq, s, Hq, 128), 90 + i) for i, s in enumerate((Sq, Skv, Skv)))
+    rows = _random_rows(Bq * Hq * nqb, nkb, phase, seed=phase * 10 + len(mode))
+    read = torch.from_numpy(rows).view(Bq, Hq, nqb, nkb + 2).to(DEV)
+    write = torch.full_like(read, -7)
+    out = ma.forward_lite(q.to(DEV), k.to(DEV), v.to(DEV), read, write, threshold=-6.0, phase=phase,
+                          round_mode=mode, layout="bshd")
+    torch.cuda.synchronize()
+    got_rows = write.cpu().numpy().reshape(-1, nkb + 2)
+    got = to_bhsd(bits(out), "bshd")
+    qf, kf, vf = (to_bhsd(f32(t), "bshd") for t in (q, k, v))
+    stats = []
+    for w in range(Bq * Hq * nqb):
+        bh, t = divmod(w, nqb)
+        b, h = divmod(bh, Hq)
+        r0, r1 = t * 256, min(Sq, (t + 1) * 256)
+        o, nxt, blocks = ol.step_tile(qf[b, h, r0:r1], kf[b, h], vf[b, h], rows[w], phase, -6.0,
+                                      {"rtne": 0, "rtna": 1, "rtz": 2}[mode], aux=True)
+        assert list(got_rows[w, :1 + nxt[0]]) == nxt, (w, blocks)
+        ref, _, scl, tie = o
+        stats.append(compare_bf16(got[b, h, r0:r1], ref, scl, tie, fractions=False))
+    agg = aggregate_stats(stats)
+    log_stats(f"lite_step_2x3_sq700_skv1500_phase{phase}_{mode}", agg)
+    check_fractions(agg)
+    assert any(len(ol.decode(r, nkb, phase)[0]) < nkb for r in rows)
+
+
+def test_lite_lpt_order_matches_oracle():
+    """The planning kernel's CTA permutation (through the C ABI) against the
+    oracle's stable heaviest-first order, on rows of very different weights."""
+    Bq, Hq, Sq, Skv = 1, 6, 1024, 4096
+    nqb, nkb = Sq // 256, Skv // 64
+    rng = np.random.default_rng(5)
+    rows = np.zeros((Bq * Hq * nqb, nkb + 2), np.int16)
+    for i in range(len(rows)):
+        kept = int(rng.integers(1, nkb + 1))
+        rows[i, :3] = (2, kept - 1, -1)
+    q, k, v = (randn_bf16((Bq, s, Hq, 128), 50 + i).to(DEV) for i, s in enumerate((Sq, Skv, Skv)))
+    vt = torch.empty(_lib.lib.moonmath_attention_vt_bytes(Bq, Hq, Skv) // 2, dtype=torch.bfloat16, device=DEV)
+    st = _lib.stream_ptr(DEV)
+    assert _lib.lib.launch_v_transpose_rtne(_lib.ptr(v), _lib.ptr(vt), Bq * Hq * Skv, Skv, Hq, 1, st) == 0
+    read = torch.from_numpy(rows).to(DEV)
+    write = torch.zeros_like(read)
+    out = torch.empty_like(q)
+    ws = torch.full((_lib.lib.lite_workspace_bytes_rtne(Bq, Hq, Sq) // 4,), -1, dtype=torch.int32, device=DEV)
+    rc = _lib.lib.launch_attention_forward_lite_rtne(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), Bq, Hq, Sq, Skv, 128, _lib.ptr(read),
+        _lib.ptr(write), None, -6.0, 1, 1, _lib.ptr(ws), st)
+    torch.cuda.synchronize()
+    assert rc == 0
+    assert ws.cpu().tolist() == ol.lpt_order(rows, nkb)
+
+
+def test_forward_lite_rejects_bad_lists():
+    q, k, v = _uniform("bhsd")
+    nqb, nkb = S // 256, S // 64
+    good = torch.zeros(B, H, nqb, nkb + 2, dtype=torch.int16, device=DEV)
+    with pytest.raises(ValueError, match="int16"):
+        ma.forward_lite(q, k, v, good.int(), good, threshold=-3.0, phase=1)
+    with pytest.raises(ValueError, match="at least"):
+        ma.forward_lite(q, k, v, good[..., :-1].contiguous(), good, threshold=-3.0, phase=1)
+    with pytest.raises(ValueError, match="same device"):
+        ma.forward_lite(q, k, v, good, good.cpu(), threshold=-3.0, phase=1)
+    short = torch.tensor([4, 0, 5], dtype=torch.int16, device=DEV)
+    with pytest.raises(ValueError, match="must_do_list"):
+        ma.forward_lite(q, k, v, good, good.clone(), threshold=-3.0, phase=1, must_do_list=short)
