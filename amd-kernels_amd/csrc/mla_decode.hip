@@ -672,6 +672,38 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
   *reinterpret_cast<u32x2*>(p.o_lat + ((long long)qb * p.qrows + qrow) * kLat + d) = o;
 }
 
+// ---------------------------------------------------------------------------
+// 64-token block tables -> the flat per-token slots the decode reads. Request
+// b's slots go at stride max_blocks * 64: idx[b * stride + t] = page(b, t / 64)
+// * 64 + t % 64 for t < len_b, with page ids clamped to the pool and
+// len_b = seq_lens[b] clamped to [0, max_blocks * 64], so no table content
+// makes the decode read outside the pool. Index workspace (int32):
+// [B * stride slots][B lengths][B + 1 offsets]. One thread per token slot of
+// the table (4 pages per 256-thread CTA).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void expand_block_table_kernel(const int* __restrict__ seq_lens,
+                                                                 const int* __restrict__ table, int max_blocks,
+                                                                 int num_blocks, int B, int* __restrict__ ws) {
+  const long long page = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (page >= (long long)B * max_blocks) return;
+  const int b = (int)(page / max_blocks), j = (int)(page % max_blocks);
+  const long long stride = (long long)max_blocks * 64;
+  int len = seq_lens[b];
+  len = len < 0 ? 0 : (len > stride ? (int)stride : len);
+  const int t = j * 64 + lane;
+  if (t < len) {
+    int blk = table[page];
+    blk = blk < 0 ? 0 : (blk >= num_blocks ? num_blocks - 1 : blk);
+    ws[b * stride + t] = blk * 64 + lane;
+  }
+  if (j == 0 && lane == 0) {
+    ws[B * stride + b] = len;
+    ws[B * stride + B + b] = (int)(b * stride);
+    if (b == B - 1) ws[B * stride + 2 * B] = (int)(B * stride);
+  }
+}
+
 // Test hook: decode fp8 bytes with the same hardware convert the kernel uses.
 __global__ void fp8_to_bf16_kernel(const uint8_t* in, uint16_t* out, int n) {
   const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -901,6 +933,33 @@ int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_p
   }
   return launch(q_lat, q_pe, kv_pool, o_lat, seq_lens, rows, kv_indices, kv_indptr, B, H, 0, eff, q_len, lat_dim,
                 rope_dim, scale, kv_scale, ws, stream, true);
+}
+
+size_t mla_decode_a16w8_blocks_index_bytes(int B, int max_blocks) {
+  if (B < 1 || max_blocks < 1) return 0;
+  return ((size_t)B * max_blocks * 64 + 2 * (size_t)B + 1) * sizeof(int);
+}
+
+int launch_mla_decode_a16w8_paged_blocks_dev(const void* q_lat, const void* q_pe, const void* kv_pool, void* o_lat,
+                                             const void* seq_lens, const void* rows, const void* block_table,
+                                             int max_blocks, int num_blocks, int B, int H, int parts, int q_len,
+                                             int lat_dim, int rope_dim, float scale, float kv_scale, float scale_p,
+                                             void* workspace, void* index_workspace, void* stream) {
+  (void)scale_p;
+  if (!seq_lens || !block_table || !index_workspace) return -6;
+  if (B < 1 || B > kMaxPagedB) return -4;
+  if (max_blocks < 1 || num_blocks < 1) return -11;
+  const long long words = (long long)B * max_blocks * 64 + 2LL * B + 1;
+  if (words > 0x7FFFFFFFLL || (long long)num_blocks * 64 > 0x7FFFFFFFLL) return -11;
+  int* ws = static_cast<int*>(index_workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const long long pages = (long long)B * max_blocks;
+  hipLaunchKernelGGL(expand_block_table_kernel, dim3((unsigned)((pages + 3) / 4)), dim3(256), 0, st,
+                     static_cast<const int*>(seq_lens), static_cast<const int*>(block_table), max_blocks, num_blocks,
+                     B, ws);
+  const long long stride_all = (long long)B * max_blocks * 64;
+  return launch(q_lat, q_pe, kv_pool, o_lat, ws + stride_all, rows, ws, ws + stride_all + B, B, H, 0, parts, q_len,
+                lat_dim, rope_dim, scale, kv_scale, workspace, stream, true);
 }
 
 int launch_mla_decode_a16w8_multiq(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, int B, int H,

@@ -16,6 +16,7 @@ from .mla import (
     mla_decode_a16w8_multiq,
     mla_decode_a16w8_multiq_paged_dev,
     mla_decode_a16w8_multiq_plan_parts_q,
+    mla_decode_a16w8_paged_blocks,
     mla_decode_a16w8_paged_dev,
     mla_decode_a16w8_plan_parts,
     mla_decode_a16w8_plan_parts_capped,
@@ -24,7 +25,7 @@ from .mla import (
 
 __all__ = [
     "forward", "forward_lite", "LiteAttention",
-    "mla_decode_a16w8", "mla_decode_a16w8_paged_dev",
+    "mla_decode_a16w8", "mla_decode_a16w8_paged_dev", "mla_decode_a16w8_paged_blocks",
     "mla_decode_a16w8_plan_parts", "mla_decode_a16w8_plan_parts_capped",
     "mla_decode_a16w8_plan_parts_q",
     "mla_decode_a16w8_multiq", "mla_decode_a16w8_multiq_paged_dev",

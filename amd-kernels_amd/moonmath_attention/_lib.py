@@ -40,6 +40,9 @@ SIGNATURES.update({
         _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _f, _p, _p, _sz, _i]),
     "launch_mla_decode_a16w8_paged_dev_noalloc": (
         _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f, _f, _p, _sz, _i]),
+    "mla_decode_a16w8_blocks_index_bytes": (_sz, [_i, _i]),
+    "launch_mla_decode_a16w8_paged_blocks_dev": (
+        _i, [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _f, _p, _p, _p]),
     "launch_mla_decode_a16w8_multiq": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _f, _p, _p]),
     "launch_mla_decode_a16w8_multiq_paged_dev": (
         _i, [_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _f, _p, _p, _sz]),

@@ -24,6 +24,7 @@ from . import _lib
 __all__ = [
     "mla_decode_a16w8",
     "mla_decode_a16w8_paged_dev",
+    "mla_decode_a16w8_paged_blocks",
     "mla_decode_a16w8_plan_parts",
     "mla_decode_a16w8_plan_parts_capped",
     "mla_decode_a16w8_plan_parts_q",
@@ -178,6 +179,61 @@ def mla_decode_a16w8_paged_dev(q_lat, q_pe, kv_pool, o_lat, seq_lens, rows, kv_i
              _lib.ptr(o_lat), _lib.ptr(seq_lens), _lib.ptr(rows), _lib.ptr(kv_indices), _lib.ptr(kv_indptr),
              B, H, int(parts), _LAT, _ROPE, float(scale), float(kv_scale), float(scale_p), _lib.ptr(ws),
              _lib.stream_ptr(dev), kv_indices.numel() * _QK, q_len)
+
+
+_PAGE = 64
+
+
+def mla_decode_a16w8_paged_blocks(q_lat, q_pe, kv_pool, o_lat, seq_lens, block_table, parts, scale, kv_scale,
+                                  scale_p=1.0, rows=None) -> None:
+    """Absorbed decode over a paged pool addressed by 64-token block tables (the
+    form a serving stack's paged KV cache keeps; no counterpart in the
+    reference, whose ops take flat per-token slots).
+
+    kv_pool: float8_e4m3fn pages of 64 fused rows, [num_blocks, 64, 576] (or
+    any contiguous shape of num_blocks * 64 rows of 576); block_table: int32
+    [B, max_blocks], request b's token t is row t % 64 of page
+    block_table[b, t // 64]; q_lat [B,H,512] (q_len 1) or [B,q_len,H,512]
+    (q_len <= 8), draft window end-aligned; rows as in the paged ops. Device
+    driven and graph capturable with ``parts`` fixed: the table is expanded to
+    per-token slots on the GPU (page ids clamped to the pool, lengths to the
+    table) and the flat-slot decode runs on the same stream.
+    """
+    who = "mla_decode_a16w8_paged_blocks"
+    B, H, q_len = _check_q(q_lat, q_pe, o_lat, who, multiq=False)
+    if not isinstance(kv_pool, torch.Tensor) or kv_pool.dtype != _FP8:
+        raise ValueError(f"{who}: kv_pool must be float8_e4m3fn")
+    if kv_pool.shape[-1] != _QK or kv_pool.numel() % (_PAGE * _QK) != 0 or not kv_pool.is_contiguous():
+        raise ValueError(f"{who}: kv_pool must be contiguous pages of 64 rows of 576 ([num_blocks,64,576])")
+    if not isinstance(block_table, torch.Tensor) or block_table.dtype != torch.int32 or block_table.dim() != 2:
+        raise ValueError(f"{who}: block_table must be int32 [B, max_blocks]")
+    if block_table.shape[0] != B or not block_table.is_contiguous() or block_table.shape[1] < 1:
+        raise ValueError(f"{who}: block_table must be contiguous [B, max_blocks] with B = q_lat's batch")
+    if not isinstance(seq_lens, torch.Tensor) or seq_lens.dtype != torch.int32 or not seq_lens.is_contiguous():
+        raise ValueError(f"{who}: seq_lens must be contiguous int32")
+    if seq_lens.numel() < B:
+        raise ValueError(f"{who}: seq_lens must have >= B entries")
+    for name, t in (("kv_pool", kv_pool), ("block_table", block_table), ("seq_lens", seq_lens)):
+        if t.device != q_lat.device:
+            raise ValueError(f"{who}: {name} must be on q_lat's device")
+    if rows is not None:
+        if not isinstance(rows, torch.Tensor) or rows.dtype != torch.int32 or rows.numel() < B:
+            raise ValueError(f"{who}: rows must be int32 with >= B entries")
+        if rows.device != q_lat.device or not rows.is_contiguous():
+            raise ValueError(f"{who}: rows must be contiguous on q_lat's device")
+    if int(parts) > (1 << 20):
+        raise ValueError(f"{who}: parts is absurd (> 2^20)")
+    num_blocks = kv_pool.numel() // (_PAGE * _QK)
+    max_blocks = block_table.shape[1]
+    dev = q_lat.device
+    lib = _lib.lib
+    with torch.cuda.device(dev):
+        ws = _workspace(B, H, parts, q_len, dev)
+        idx_ws = torch.empty(lib.mla_decode_a16w8_blocks_index_bytes(B, max_blocks), dtype=torch.uint8, device=dev)
+        _run("launch_mla_decode_a16w8_paged_blocks_dev", _lib.ptr(q_lat), _lib.ptr(q_pe), _lib.ptr(kv_pool),
+             _lib.ptr(o_lat), _lib.ptr(seq_lens), _lib.ptr(rows), _lib.ptr(block_table), max_blocks, num_blocks,
+             B, H, int(parts), q_len, _LAT, _ROPE, float(scale), float(kv_scale), float(scale_p), _lib.ptr(ws),
+             _lib.ptr(idx_ws), _lib.stream_ptr(dev))
 
 
 def mla_decode_a16w8_plan_parts(B: int, H: int, max_seq_len: int, lat_dim: int = 512) -> int:

@@ -111,7 +111,7 @@ size_t moonmath_attention_vt_bytes(int batch, int heads, int seq_len_kv);
  * place. H in [1,128], q_len in [1,8]. Codes: -2 lat/rope dims, -3 H,
  * -4 q_len or B, -6 null pointer, -7 S < 1, -8 grid overflow, -9 split
  * records beyond the allocation-free entry point's array, -10 no device
- * address for that array.
+ * address for that array, -11 bad block-table geometry.
  * ------------------------------------------------------------------------- */
 
 /* Fixed split-workspace cap in bytes. Replaces csrc/mla_decode_a16w8.hip:178-181. */
@@ -152,6 +152,24 @@ int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_p
                                               const void* kv_indptr, int B, int H, int parts, int lat_dim,
                                               int rope_dim, float scale, float kv_scale, float scale_p, void* stream,
                                               size_t kv_bytes, int q_len);
+
+/* Paged decode over 64-token block tables: kv_pool holds num_blocks pages of
+ * 64 fused 576-byte rows; request b's token t lives in page
+ * block_table[b * max_blocks + t / 64], row t % 64; q_len 1..8 as in
+ * launch_mla_decode_a16w8_paged_dev (rows, parts, workspace likewise).
+ * index_workspace: mla_decode_a16w8_blocks_index_bytes(B, max_blocks) bytes
+ * into which the table is expanded to per-token slots (page ids clamped to
+ * [0, num_blocks), lengths to [0, max_blocks * 64]) before the decode, on the
+ * same stream. Codes: as the paged launcher, plus -11 (max_blocks or
+ * num_blocks < 1, or tables beyond int32 indexing). No counterpart in the
+ * reference, whose decode takes flat per-token slots only: this is the
+ * block-table form a serving stack's paged KV cache keeps. */
+size_t mla_decode_a16w8_blocks_index_bytes(int B, int max_blocks);
+int launch_mla_decode_a16w8_paged_blocks_dev(const void* q_lat, const void* q_pe, const void* kv_pool, void* o_lat,
+                                             const void* seq_lens, const void* rows, const void* block_table,
+                                             int max_blocks, int num_blocks, int B, int H, int parts, int q_len,
+                                             int lat_dim, int rope_dim, float scale, float kv_scale, float scale_p,
+                                             void* workspace, void* index_workspace, void* stream);
 
 /* Multi-query (draft window) contiguous decode. Replaces
  * csrc/mla_decode_a16w8_multiq.hip:955-983. */
