@@ -21,6 +21,7 @@ from .mla import (
     mla_decode_a16w8_plan_parts,
     mla_decode_a16w8_plan_parts_capped,
     mla_decode_a16w8_plan_parts_q,
+    mla_kv_quantize,
 )
 
 __all__ = [
@@ -29,5 +30,5 @@ __all__ = [
     "mla_decode_a16w8_plan_parts", "mla_decode_a16w8_plan_parts_capped",
     "mla_decode_a16w8_plan_parts_q",
     "mla_decode_a16w8_multiq", "mla_decode_a16w8_multiq_paged_dev",
-    "mla_decode_a16w8_multiq_plan_parts_q",
+    "mla_decode_a16w8_multiq_plan_parts_q", "mla_kv_quantize",
 ]

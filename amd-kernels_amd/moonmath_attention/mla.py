@@ -31,6 +31,7 @@ __all__ = [
     "mla_decode_a16w8_multiq",
     "mla_decode_a16w8_multiq_paged_dev",
     "mla_decode_a16w8_multiq_plan_parts_q",
+    "mla_kv_quantize",
 ]
 
 _LAT = 512
@@ -289,3 +290,47 @@ def mla_decode_a16w8_multiq_paged_dev(q_lat, q_pe, kv_pool, o_lat, seq_lens, row
 def mla_decode_a16w8_multiq_plan_parts_q(B: int, max_seq_len: int, q_len: int = 4, H: int = 16) -> int:
     """Fixed KV-split count for a multi-query graph captured at (B, max_seq_len, q_len, H)."""
     return int(_lib.lib.mla_decode_a16w8_multiq_plan_parts_q(int(B), int(max_seq_len), int(q_len), int(H)))
+
+
+def mla_kv_quantize(c_kv, k_pe, kv_pool, slots, kv_scale, saturate=False) -> None:
+    """Write new tokens into the fp8 KV cache the decode ops read.
+
+    c_kv [N, 512] and k_pe [N, 64] bf16 (latent and roped key of N tokens);
+    kv_pool float8_e4m3fn with rows of 576 ([num_slots, 576], [num_slots, 1,
+    576] or [num_blocks, 64, 576]); slots int32 [N]: token i goes to row
+    slots[i] (negative = padding token, skipped). Each row becomes
+    e4m3fn(x / kv_scale) of [c_kv | k_pe], round to nearest even, |x / kv_scale|
+    > 464 -> NaN as torch's float8_e4m3fn cast, or clamped to +-448 with
+    ``saturate``. Written in place on the current stream (graph capturable).
+    The reference has no producer; this is the cache format its ops take
+    (moonmath_attention/mla.py:17-20) filled the way its tests fill it
+    (tests/test_mla_decode.py:34-38).
+    """
+    who = "mla_kv_quantize"
+    for name, t, w in (("c_kv", c_kv, _LAT), ("k_pe", k_pe, _ROPE)):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16:
+            raise ValueError(f"{who}: {name} must be a bfloat16 tensor")
+        if t.dim() < 1 or t.shape[-1] != w or not t.is_contiguous():
+            raise ValueError(f"{who}: {name} must be contiguous [..., {w}]")
+    N = c_kv.numel() // _LAT
+    if k_pe.numel() // _ROPE != N:
+        raise ValueError(f"{who}: c_kv and k_pe must hold the same number of tokens")
+    if not isinstance(kv_pool, torch.Tensor) or kv_pool.dtype != _FP8:
+        raise ValueError(f"{who}: kv_pool must be float8_e4m3fn")
+    if kv_pool.shape[-1] != _QK or not kv_pool.is_contiguous():
+        raise ValueError(f"{who}: kv_pool must be contiguous rows of 576")
+    if not isinstance(slots, torch.Tensor) or slots.dtype != torch.int32 or not slots.is_contiguous():
+        raise ValueError(f"{who}: slots must be contiguous int32")
+    if slots.numel() != N:
+        raise ValueError(f"{who}: slots must have one entry per token ({N}), got {slots.numel()}")
+    for name, t in (("k_pe", k_pe), ("kv_pool", kv_pool), ("slots", slots)):
+        if t.device != c_kv.device:
+            raise ValueError(f"{who}: {name} must be on c_kv's device")
+    if c_kv.device.type != "cuda":
+        raise ValueError(f"{who}: tensors must be on a CUDA/HIP device")
+    if not (float(kv_scale) > 0.0) or float(kv_scale) == float("inf"):
+        raise ValueError(f"{who}: kv_scale must be a positive finite number")
+    dev = c_kv.device
+    with torch.cuda.device(dev):
+        _run("launch_mla_kv_quantize", _lib.ptr(c_kv), _lib.ptr(k_pe), _lib.ptr(kv_pool), _lib.ptr(slots), N,
+             kv_pool.numel() // _QK, float(kv_scale), int(bool(saturate)), _lib.stream_ptr(dev))

@@ -285,11 +285,25 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1)), c
         if cpu:
             rec["cpu_baseline"] = mla_cpu_baseline(torch, qs_cpu[0], cpu_sets[0], lens, nbytes, flops)
         results.append(rec)
+    # The fp8 KV producer filling the whole batch's cache: every token of the
+    # 64 requests quantised from bf16 latent / rope into its pool slot
+    # (HBM-bound: 1152 B read + 576 B written + 4 B of slot per token).
+    g = torch.Generator(device="cuda:0").manual_seed(6)
+    c_kv = torch.randn(sum_l, 512, generator=g, device="cuda:0").to(torch.bfloat16)
+    k_pe = torch.randn(sum_l, 64, generator=g, device="cuda:0").to(torch.bfloat16)
+    pool, idx, _ = sets[0]
+    us = _time(torch, lambda i: ma.mla_kv_quantize(c_kv, k_pe, pool, idx, KV_SCALE), steps, warmup) * 1e3
+    qbytes = sum_l * (1152 + 576 + 4)
+    qgbs = qbytes / (us * 1e-6) / 1e9
+    producer = {"tokens": sum_l, "us": round(us, 2), "bytes": qbytes, "hbm_GBs": round(qgbs, 1),
+                "pct_hbm_peak": round(100 * qgbs / PEAK_HBM_GBS, 2), "kv_scale": KV_SCALE}
+    _log(f"bench: mla kv producer {sum_l} tokens: {us:.1f} us, {qgbs:.0f} GB/s")
     return {
         "metric": "MLA decode HBM GB/s (% peak)",
         "workload": "B=64 ctx~U[1024,8192] (seed 5) 64-token pages, fp8 e4m3fn KV, 3 rotating pools",
         "sum_ctx": sum_l,
         "configs": results,
+        "kv_producer": producer,
     }
 
 

@@ -197,6 +197,20 @@ int mla_decode_a16w8_max_ctas(void);
  * workspace (have_workspace != 0) or none. */
 int moonmath_mla_effective_parts(int B, int H, int parts, int q_len, int have_workspace);
 
+/* fp8 KV producer: for each token i < n_tokens with 0 <= slots[i] < num_slots,
+ * writes row slots[i] of kv_pool ([num_slots, 576] bytes) as
+ * e4m3fn(fl32(x / kv_scale)) of c_kv[i, 0:512] then k_pe[i, 0:64] (bf16,
+ * contiguous [n, 512] and [n, 64]); round to nearest even, |x| > 464 -> NaN
+ * (saturate == 0, torch's float8_e4m3fn cast) or +-448 (saturate != 0).
+ * Other rows are not touched (slot -1 marks a padding token). Codes: -4
+ * negative sizes, -6 null pointer, -8 grid overflow, -12 kv_scale not a
+ * positive finite number. The reference has no producer; this writes its
+ * cache format (moonmath_attention/mla.py:17-20,
+ * csrc/mla_decode_a16w8_api.cpp:5-8) the way its tests fill it
+ * (tests/test_mla_decode.py:34-38). */
+int launch_mla_kv_quantize(const void* c_kv, const void* k_pe, void* kv_pool, const void* slots, long long n_tokens,
+                           long long num_slots, float kv_scale, int saturate, void* stream);
+
 /* Test hook: decode n OCP e4m3fn bytes to bf16 bits with the kernel's
  * hardware convert (v_cvt_scalef32_pk_bf16_fp8, scale 1). */
 int moonmath_fp8e4m3_to_bf16(const void* in, void* out, int n, void* stream);

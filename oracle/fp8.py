@@ -32,3 +32,27 @@ DECODE = _table()
 def decode(u8):
     """uint8 array of e4m3fn bit patterns -> float64 values."""
     return DECODE[np.asarray(u8, dtype=np.uint8)]
+
+
+def encode(x_f32, saturate=False):
+    """float32 array -> e4m3fn bits (uint8) with torch's float8_e4m3fn cast
+    (round to nearest even; |x| > 464 -> NaN, NaN -> NaN). With ``saturate``
+    every non-NaN value is first clamped to [-448, 448] (the OCP "satfinite"
+    conversion)."""
+    import torch
+
+    x = torch.from_numpy(np.ascontiguousarray(np.asarray(x_f32, dtype=np.float32)))
+    if saturate:
+        x = torch.where(torch.isnan(x), x, x.clamp(-448.0, 448.0))
+    return x.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def quantize_rows(c_kv_f32, k_pe_f32, kv_scale, saturate=False):
+    """The KV producer's rows: encode(fl32(x / kv_scale)) of [c_kv | k_pe]
+    (fp32 division, as the reference's tests fill the cache,
+    tests/test_mla_decode.py:34-38). Inputs [N, 512] / [N, 64] float32."""
+    import torch
+
+    x = torch.cat([torch.from_numpy(np.asarray(c_kv_f32, np.float32)),
+                   torch.from_numpy(np.asarray(k_pe_f32, np.float32))], dim=1)
+    return encode((x / np.float32(kv_scale)).numpy(), saturate)

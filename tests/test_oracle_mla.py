@@ -109,3 +109,42 @@ def test_torch_formula_cpu_matches_numpy_fp32_reference():
     ref = om.fp32_reference(q_lat.float().numpy(), q_pe.float().numpy(), pool.view(torch.uint8).numpy(), lens,
                             SCALE_576, KV_SCALE, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+# fp32 value -> expected e4m3fn bits, derived by hand from the OCP spec:
+# 1.0 = 0.0111.000; 448 = max finite 0.1111.110; 464 = halfway 448..480 -> even
+# (448); above it no finite value is nearer -> NaN (torch's cast); 2^-6 =
+# smallest normal 0.0001.000; 2^-9 = smallest subnormal; 2^-10 = halfway 0..2^-9
+# -> even (0); 1.5 * 2^-10 -> 2^-9; 1.0625 = 1 + 1/16, halfway 1..1.125 -> 1.0;
+# -3 = -1.5 * 2^1 = 1.1000.100, -2 = 1.1000.000;
+# 1.1875 halfway 1.125..1.25 -> even mantissa (1.25 = 0.0111.010).
+ENCODE_KAT = [
+    (1.0, 0x38, 0x38), (448.0, 0x7E, 0x7E), (464.0, 0x7E, 0x7E), (465.0, 0x7F, 0x7E), (1e6, 0x7F, 0x7E),
+    (-1e6, 0xFF, 0xFE), (np.inf, 0x7F, 0x7E), (-np.inf, 0xFF, 0xFE), (2.0 ** -6, 0x08, 0x08),
+    (2.0 ** -9, 0x01, 0x01), (2.0 ** -10, 0x00, 0x00), (1.5 * 2.0 ** -10, 0x01, 0x01), (1.0625, 0x38, 0x38),
+    (1.1875, 0x3A, 0x3A), (-0.0, 0x80, 0x80), (0.0, 0x00, 0x00), (-3.0, 0xC4, 0xC4), (-2.0, 0xC0, 0xC0),
+]
+
+
+@pytest.mark.parametrize("x,plain,sat", ENCODE_KAT)
+def test_fp8_encode_known_answers(x, plain, sat):
+    assert int(of8.encode(np.array([x]))[0]) == plain
+    assert int(of8.encode(np.array([x]), saturate=True)[0]) == sat
+
+
+def test_fp8_encode_nan_and_round_trip_of_every_code():
+    assert (int(of8.encode(np.array([np.nan]))[0]) & 0x7F) == 0x7F
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    assert np.array_equal(of8.encode(of8.decode(codes).astype(np.float32)), codes)
+
+
+def test_quantize_rows_divides_in_fp32():
+    """kv_scale 0.1 is not a power of two: the row is encode(fl32(x / 0.1)),
+    which differs from encode(fl32(x * fl32(1/0.1))) on some inputs."""
+    g = np.random.default_rng(4)
+    c = g.standard_normal((64, 512)).astype(np.float32)
+    r = g.standard_normal((64, 64)).astype(np.float32)
+    got = of8.quantize_rows(c, r, 0.1)
+    x = np.concatenate([c, r], axis=1)
+    assert np.array_equal(got, of8.encode((x / np.float32(0.1)).astype(np.float32)))
+    assert got.shape == (64, 576)
