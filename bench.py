@@ -12,7 +12,7 @@ the reference repo's CPU oracle formula (examples/basic.py:16-17) over the
 whole headline workload on this host's cores (median of 3). Extra keys:
 ``attention`` (every round mode, the reference benchmark's "realistic" inputs,
 the configs[3] long shapes, a shape whose tail KV-split fires, with and
-without the split) and ``mla`` (configs[4] decode lines with their own CPU
+without the split, the configs[2] cross-attention shapes) and ``mla`` (configs[4] decode lines with their own CPU
 baseline, the reference test's fp32 formula).
 """
 import argparse
@@ -140,7 +140,8 @@ def _leg(name, B, H, Sq, Skv, ms, **extra):
 
 def bench_attention_extra(args, torch, ma, qkv_cpu):
     """Other round modes, the reference benchmark's input pattern, the long
-    configs and the tail KV-split (one `forward` call per step, as the headline)."""
+    configs, the tail KV-split and the cross-attention configs (one `forward`
+    call per step, as the headline)."""
     sys.path.insert(0, str(ROOT / "tests"))
     from helpers import realistic_bf16
 
@@ -184,6 +185,22 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
         finally:
             os.environ.pop("MOONMATH_NO_TAIL", None)
         res[f"tail_{label}_2x24_sq4097_skv8192_rtne"] = _leg(f"tail {label}", B, H, Sq, Skv, ms, round_mode="rtne")
+    del q, k, v, o
+    # cross-attention, Q ~ N(0,1), K/V ~ 0.5 N(0,1). Short KV ranges
+    # make these shapes partly HBM-bound (Q in, O out), so the leg also reports
+    # the algorithmic bytes (q, k, v, out once) per second.
+    for Sq, Skv in ((8192, 512), (8192, 77), (4097, 512)):
+        g.manual_seed(23)
+        q = torch.randn(2, Sq, 24, 128, generator=g, device="cuda:0").to(torch.bfloat16)
+        k, v = ((0.5 * torch.randn(2, Skv, 24, 128, generator=g, device="cuda:0")).to(torch.bfloat16) for _ in range(2))
+        o = torch.empty_like(q)
+        ms = _time(torch, lambda i: ma.forward(q, k, v, out=o, round_mode="rtne", layout="bshd"), args.steps,
+                   args.warmup)
+        nbytes = 2 * 24 * 128 * 2 * (2 * Sq + 2 * Skv)
+        res[f"cross_2x24_sq{Sq}_skv{Skv}_rtne"] = _leg(
+            f"cross sq{Sq} skv{Skv}", 2, 24, Sq, Skv, ms, round_mode="rtne", hbm_bytes=nbytes,
+            hbm_GBs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        del q, k, v, o
     return res
 
 
