@@ -11,8 +11,8 @@
 // `saturate`, clamped to +-448 (NaN stays NaN).
 //
 // HBM-bound: 1152 bytes read and 576 written per token. One thread per 16
-// output bytes (two 16-byte bf16 loads, one 16-byte store); the 36 threads of
-// a row write its 576 bytes contiguously.
+// output bytes (two 16-byte bf16 loads, 8 hardware converts, one 16-byte
+// store); the 36 threads of a row write its 576 bytes contiguously.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -28,35 +28,26 @@ constexpr int kThreads = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// fp32 -> OCP e4m3fn (bias 7, no infinities, 0x7F / 0xFF = NaN, max 448),
-// round to nearest even. Overflow (|x| > 464, the midpoint past 448) -> NaN,
-// or +-448 when saturating.
-__device__ __forceinline__ uint32_t f32_to_e4m3fn(float f, bool saturate) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return sign | 0x7Fu;                  // NaN
-  if (a > 0x43E80000u) return sign | (saturate ? 0x7Eu : 0x7Fu);  // |x| > 464 (incl. inf)
-  if (a >= 0x3C800000u) {                                     // |x| >= 2^-6: normal
-    // Keep 3 mantissa bits, round to nearest even on the 20 dropped bits; a
-    // carry into the exponent is the correctly rounded result.
-    const uint32_t r = (a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20;
-    return sign | (r - (120u << 3));                          // rebias 127 -> 7
-  }
-  // Subnormal (or zero): |x| / 2^-9 rounded to nearest even, 0..8 (8 is the
-  // smallest normal, encoded the same way).
-  const float m = __builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
-  return sign | (uint32_t)m;
+// fp32 -> OCP e4m3fn, two values per instruction: v_cvt_scalef32_pk_fp8_f32
+// at scale 1 rounds to nearest even, keeps subnormals, and turns NaN and
+// magnitudes above 464 (the midpoint past 448, infinities included) into a
+// NaN code (0x7F / 0xFF), which is torch's non-saturating cast (checked
+// against a bit-level encoder on every bf16 pattern at several scales).
+// Saturating callers clamp |x| > 448 to +-448 first (a NaN fails the compare
+// and stays NaN).
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float clamp448(float x) {
+  return __builtin_fabsf(x) > 448.f ? __builtin_copysignf(448.f, x) : x;
 }
 
 // POW2: kv_scale is a power of two, so x / kv_scale == x * (1 / kv_scale)
 // exactly and the correctly rounded division is replaced by one multiply.
-template <bool POW2>
+template <bool POW2, bool SAT>
 __global__ __launch_bounds__(kThreads) void kv_quant_kernel(const uint16_t* __restrict__ c_kv,
                                                             const uint16_t* __restrict__ k_pe,
                                                             uint8_t* __restrict__ pool, const int* __restrict__ slots,
                                                             long long n_tokens, long long num_slots, float kv_scale,
-                                                            float inv_scale, int saturate) {
+                                                            float inv_scale) {
   const long long item = (long long)blockIdx.x * kThreads + threadIdx.x;
   if (item >= n_tokens * kChunks) return;
   const long long tok = item / kChunks;
@@ -64,25 +55,24 @@ __global__ __launch_bounds__(kThreads) void kv_quant_kernel(const uint16_t* __re
   const long long slot = slots[tok];
   if (slot < 0 || slot >= num_slots) return;  // padding token / outside the pool: nothing written
   const uint16_t* src = chunk < kLat / 16 ? c_kv + tok * kLat + chunk * 16 : k_pe + tok * kRope + (chunk - kLat / 16) * 16;
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(src);      // elements 0..7
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(src + 8);  // elements 8..15
-  const bool sat = saturate != 0;
+  // Inputs are read once and rows written once: non-temporal accesses.
+  const u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));      // elements 0..7
+  const u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 8));  // elements 8..15
+  auto val = [&](uint32_t pair, bool upper) {  // one bf16 of a pair, widened and divided by kv_scale
+    const float xv = __builtin_bit_cast(float, upper ? (pair & 0xFFFF0000u) : (pair << 16));
+    const float x = POW2 ? xv * inv_scale : xv / kv_scale;
+    return SAT ? clamp448(x) : x;
+  };
   u32x4 out;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const u32x4& v = w < 2 ? lo : hi;  // output word w = elements 4w .. 4w+3
-    uint32_t word = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t pair = v[(w & 1) * 2 + (j >> 1)];
-      const uint32_t bf = (j & 1) ? (pair >> 16) : (pair & 0xFFFFu);
-      const float xv = __builtin_bit_cast(float, bf << 16);
-      const float x = POW2 ? xv * inv_scale : xv / kv_scale;
-      word |= f32_to_e4m3fn(x, sat) << (8 * j);
-    }
-    out[w] = word;
+    const uint32_t p0 = v[(w & 1) * 2], p1 = v[(w & 1) * 2 + 1];
+    s16x2 r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(s16x2{0, 0}, val(p0, false), val(p0, true), 1.0f, false);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, val(p1, false), val(p1, true), 1.0f, true);
+    out[w] = __builtin_bit_cast(uint32_t, r);
   }
-  *reinterpret_cast<u32x4*>(pool + slot * kRow + chunk * 16) = out;
+  __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(pool + slot * kRow + chunk * 16));
 }
 
 }  // namespace kvq
@@ -102,11 +92,12 @@ int launch_mla_kv_quantize(const void* c_kv, const void* k_pe, void* kv_pool, co
   int e2 = 0;
   const bool pow2 = __builtin_frexpf(kv_scale, &e2) == 0.5f && e2 - 1 >= -126 && e2 - 1 <= 126;
   const float inv = pow2 ? __builtin_ldexpf(1.0f, 1 - e2) : 0.f;
-  auto* kern = pow2 ? mm::kvq::kv_quant_kernel<true> : mm::kvq::kv_quant_kernel<false>;
+  auto* kern = pow2 ? (saturate ? mm::kvq::kv_quant_kernel<true, true> : mm::kvq::kv_quant_kernel<true, false>)
+                    : (saturate ? mm::kvq::kv_quant_kernel<false, true> : mm::kvq::kv_quant_kernel<false, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(mm::kvq::kThreads), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(c_kv), static_cast<const uint16_t*>(k_pe),
                      static_cast<uint8_t*>(kv_pool), static_cast<const int*>(slots), n_tokens, num_slots, kv_scale,
-                     inv, saturate);
+                     inv);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? 0 : (int)e;
 }
