@@ -103,3 +103,19 @@ def test_forward_tile_compute_all_equals_dense_oracle():
     assert np.array_equal(ol.forward_tile(q, k, v, blocks, 1), oa.head_forward(q, k, v, 1)[0])
     # descending order, same keys: same result
     assert np.array_equal(ol.forward_tile(q, k, v, blocks[::-1], 1), oa.head_forward(q, k, v, 1)[0])
+
+
+def test_forward_tile_subset_equals_dense_oracle_on_kept_keys():
+    """A skip list computes attention over exactly the keys of its kept
+    blocks: the same as the dense oracle on those keys alone (ragged last
+    block included), in either processing order."""
+    g = torch.Generator().manual_seed(5)
+    skv = 300  # 5 blocks, the last one 44 keys
+    q, k, v = (torch.randn(n, 128, generator=g).to(torch.bfloat16).float().numpy() for n in (40, skv, skv))
+    for blocks in ([0, 2, 4], [4, 1], [3]):
+        keys = np.concatenate([np.arange(64 * b, min(64 * b + 64, skv)) for b in sorted(blocks)])
+        want = oa.head_forward(q, k[keys], v[keys], 1)[0]
+        assert np.array_equal(ol.forward_tile(q, k, v, blocks, 1), want), blocks
+    # a planted mistake (off-by-one block) does not match
+    wrong = oa.head_forward(q, k[64:192], v[64:192], 1)[0]
+    assert not np.array_equal(ol.forward_tile(q, k, v, [0, 2], 1), wrong)
