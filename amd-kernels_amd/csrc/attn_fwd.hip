@@ -394,7 +394,13 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     row_m = fmaxf(block_max(sA, 0), kNegFltMax);
 
     auto step = [&](int i, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
-      const int kb = blk_of(i);
+      // Lite: the list entries of blocks i and i+3 are read before the barrier,
+      // whose lgkmcnt(0) covers their latency.
+      int kb_raw = 0, kb3_raw = 0;
+      if constexpr (LITE) {
+        kb_raw = lite_list[i];
+        kb3_raw = lite_list[i + 3 < nblk ? i + 3 : i];
+      }
       // Block i+1 has landed (block i+2 stays in flight, 4 DMAs per wave); every
       // wave is done with step i-1, so the slot of block i-1 is free.
       sched_fence();
@@ -404,11 +410,12 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       }
       sched_fence();
+      const int kb = LITE ? __builtin_amdgcn_readfirstlane(kb_raw & 0x7FFF) : kb_begin + i;
       // Block kb+3: a full block's 4 DMAs go out one per odd QK step below (all
       // 8 waves issuing theirs back to back after the barrier stall their QK);
       // a partial last block is gathered here.
       const bool dma3 = i + 3 < nblk;
-      const int kb3 = dma3 ? blk_of(i + 3) : kb;
+      const int kb3 = !dma3 ? kb : LITE ? __builtin_amdgcn_readfirstlane(kb3_raw & 0x7FFF) : kb_begin + i + 3;
       const bool dma3_full = dma3 && (kb3 + 1) * kKvBlock <= p.Skv;
       if (dma3 && !dma3_full) issue_kv(kb3, (i + 3) % kRing);
       const int pd3 = __builtin_amdgcn_readfirstlane((int)dma3_full);
@@ -520,22 +527,6 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       pack_pf(0);
       __builtin_amdgcn_s_setprio(0);
-      if constexpr (LITE) {
-        // Keep the block for the next step if some valid row's block max came
-        // within `threshold` of its running max (reference :983-995); the
-        // first processed block is always kept.
-        float bm = -__builtin_inff();
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) bm = fmaxf(bm, scur[t][e]);
-        bm = xor32_max(bm) * c;
-        const bool keep = row_valid && (bm - run_mx > p.threshold);
-        run_mx = fmaxf(run_mx, bm);
-        if ((__builtin_amdgcn_ballot_w64(keep) != 0 || i == 0) && lane == 0)
-          __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(lite_vote) + (i >> 2), (1u << wave) << ((i & 3) * 8),
-                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
       // Wave-uniform growth tests: row tile 0 and the first half of row tile 1
       // before any PV of this block, the second half of row tile 1 before its PV.
       if (__builtin_amdgcn_ballot_w64(fmaxf(lpart[0] + lpart[1], lpart[2]) > kGrowLimit) != 0) {
@@ -555,13 +546,40 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
       pack_pf(1);
-      // PV of row tile 1.
+      // PV of row tile 1; lite: with the block max of the vote (4 scores per MFMA).
+      float vmx = -__builtin_inff();
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int ss = m >> 2, dt = m & 3;
         const bf16x8 a = vb[m & 3];
         if (m + 4 < 8) vb[m & 3] = vfrag_n(8 + m + 4);
         oacc[dt] = mfma32(a, pf[1][ss], oacc[dt]);
+        if constexpr (LITE) {
+          const int e0 = 4 * (m & 3);
+          vmx = fmaxf(fmaxf(vmx, scur[m >> 2][e0]), scur[m >> 2][e0 + 1]);
+          vmx = fmaxf(fmaxf(vmx, scur[m >> 2][e0 + 2]), scur[m >> 2][e0 + 3]);
+          sched_fence();
+        }
+      }
+      if constexpr (LITE) {
+        // Keep the block for the next step if some valid row's block max came
+        // within `threshold` of its running max (reference :983-995); the
+        // first processed block is always kept. bm and bm - run_mx are each
+        // rounded to fp32 (no fused multiply-subtract).
+#pragma clang fp contract(off)
+        const float bm = xor32_max(vmx) * c;
+        const bool keep = row_valid && (bm - run_mx > p.threshold);
+        run_mx = fmaxf(run_mx, bm);
+        if ((__builtin_amdgcn_ballot_w64(keep) != 0 || i == 0) && lane == 0) {
+          // Set the wave's bit in the block's vote byte. Inline asm: the
+          // compiler would put a vmcnt(0) wait (for the in-flight K/V DMAs,
+          // which also write LDS) before an atomic it can see. The DMAs never
+          // touch the vote bytes; lite_emit reads them after lgkmcnt(0) and a
+          // barrier.
+          const uint32_t va = (uint32_t)(uintptr_t)(MM_LDS uint8_t*)(lite_vote + ((i >> 2) << 2));
+          const uint32_t vbits = (1u << wave) << ((i & 3) * 8);
+          asm volatile("ds_or_b32 %0, %1" ::"v"(va), "v"(vbits) : "memory");
+        }
       }
       row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
     };

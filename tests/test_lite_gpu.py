@@ -195,6 +195,34 @@ def test_lite_lpt_order_matches_oracle():
     assert ws.cpu().tolist() == ol.lpt_order(rows, nkb)
 
 
+@pytest.mark.parametrize("layout", ["bhsd", "bshd"])
+def test_lite_vote_rounds_product_and_difference_separately(layout):
+    """Every row's block maxima are 4 (block 0) and 3.9375 (block 1); at
+    threshold fl(fl(3.9375 c) - fl(4 c)) the oracle drops block 1, where a
+    fused multiply-subtract would keep it. One ulp lower, block 1 is kept."""
+    c = np.float32(oa.SCALE_LOG2E)
+    thr = np.float32(np.float32(3.9375) * c - np.float32(4.0) * c)
+    Sq, Skv = 256, 128
+    q = torch.zeros(1, Sq, 1, 128)
+    q[..., 0] = 1.0
+    k = torch.zeros(1, Skv, 1, 128)
+    k[:, :64, :, 0] = 4.0
+    k[:, 64:, :, 0] = 3.9375
+    v = randn_bf16((1, Skv, 1, 128), 31).float()
+    if layout == "bhsd":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    q, k, v = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    s = np.array([[4.0] * 64 + [3.9375] * 64] * Sq, np.float32)
+    for t, expect in ((thr, [True, False]), (np.nextafter(thr, np.float32(-1)), [True, True])):
+        assert ol.votes(s, [0, 1], Skv, float(t)) == expect
+        read = torch.from_numpy(ol.seed_row(2)).view(1, 1, 1, 4).to(DEV)
+        write = torch.full_like(read, -7)
+        ma.forward_lite(q, k, v, read, write, threshold=float(t), phase=1, round_mode="rtna", layout=layout)
+        torch.cuda.synchronize()
+        want = ol.emit([0, 1], [False, True], expect, 1, 2)
+        assert write.cpu().view(-1).tolist()[:1 + want[0]] == want, (float(t), expect)
+
+
 def test_forward_lite_rejects_bad_lists():
     q, k, v = _uniform("bhsd")
     nqb, nkb = S // 256, S // 64

@@ -96,6 +96,31 @@ def test_votes_keep_first_and_near_max_blocks():
     assert ol.votes(s, [3, 2, 1, 0], 256, threshold=-3.0) == [True, True, True, False]
 
 
+# Block maxima 4 and 3.9375 (bf16-exact scores); threshold = fl(fl(3.9375 c) - fl(4 c)).
+VOTE_EDGE = (4.0, 3.9375)
+
+
+def vote_edge_threshold():
+    c = np.float32(oa.SCALE_LOG2E)
+    return np.float32(np.float32(VOTE_EDGE[1]) * c - np.float32(VOTE_EDGE[0]) * c)
+
+
+def test_votes_round_the_product_and_the_difference_separately():
+    """The vote is fl(fl(bm c) - run) > thr with both roundings. At a threshold
+    equal to that difference the block is dropped, while a fused
+    multiply-subtract (one rounding; fl(3.9375 c) rounds down here) would keep
+    it: the planted fused vote below disagrees on exactly this case."""
+    from fractions import Fraction
+    c = np.float32(oa.SCALE_LOG2E)
+    thr = vote_edge_threshold()
+    s = np.array([[VOTE_EDGE[0]] * 64 + [VOTE_EDGE[1]] * 64], np.float32)
+    assert ol.votes(s, [0, 1], 128, threshold=float(thr)) == [True, False]
+    assert ol.votes(s, [0, 1], 128, threshold=float(np.nextafter(thr, np.float32(-1)))) == [True, True]
+    run = np.float32(VOTE_EDGE[0]) * c
+    fused = np.float32(float(Fraction(VOTE_EDGE[1]) * Fraction(float(c)) - Fraction(float(run))))
+    assert fused > thr  # a fused vote keeps block 1
+
+
 def test_forward_tile_compute_all_equals_dense_oracle():
     g = torch.Generator().manual_seed(3)
     q, k, v = (torch.randn(n, 128, generator=g).to(torch.bfloat16).float().numpy() for n in (40, 300, 300))
