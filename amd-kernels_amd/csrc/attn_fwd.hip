@@ -674,11 +674,25 @@ constexpr int kLptThreads = 256;
 constexpr int kLptBuckets = 64;
 constexpr int kLptMaxCtas = 65536;
 
-__device__ __forceinline__ int lite_kept(const int16_t* row, int nkb) {
-  int len = row[0];
+// Kept blocks of a read-list row: the sum of |end - start| over its pairs
+// (row[i], row[i - 1]), i = len, len - 2, ... >= 2. The length and the next
+// kLptHead - 1 entries are loaded together (rows of up to 4 pairs cost one
+// round of latency); later entries one by one. Reads stay inside the row.
+constexpr int kLptHead = 9;
+__device__ __forceinline__ void lite_row_head(const int16_t* row, int nkb, int (&e)[kLptHead]) {
+#pragma unroll
+  for (int j = 0; j < kLptHead; ++j) e[j] = row[j <= nkb + 1 ? j : nkb + 1];
+}
+__device__ __forceinline__ int lite_kept(const int16_t* row, int nkb, const int (&e)[kLptHead]) {
+  int len = e[0];
   len = len < 0 ? 0 : (len > nkb + 1 ? nkb + 1 : len);
   int kept = 0;
-  for (int i = len; i >= 2; i -= 2) {
+#pragma unroll
+  for (int i = 2; i < kLptHead; ++i) {
+    const int d = e[i] - e[i - 1];
+    kept += (i <= len && ((len - i) & 1) == 0) ? (d < 0 ? -d : d) : 0;
+  }
+  for (int i = len; i >= kLptHead; i -= 2) {
     const int d = (int)row[i] - (int)row[i - 1];
     kept += d < 0 ? -d : d;
   }
@@ -687,42 +701,59 @@ __device__ __forceinline__ int lite_kept(const int16_t* row, int nkb) {
 
 __global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const int16_t* __restrict__ read_list,
                                                                 int* __restrict__ order, int nctas, int nkb) {
-  __shared__ int hist[kLptBuckets][kLptThreads];
+  static_assert(kLptThreads == 256 && kLptBuckets == 64, "4 threads' counts per lane, one bucket per lane");
+  __shared__ __attribute__((aligned(16))) int hist[kLptBuckets][kLptThreads];
   __shared__ int bucket_base[kLptBuckets];
+  __shared__ uint8_t bk_of[kLptMaxCtas];
   const int t = threadIdx.x;
   const int chunk = (nctas + kLptThreads - 1) / kLptThreads;
   const int w0 = t * chunk;
   const int w1 = w0 + chunk < nctas ? w0 + chunk : nctas;
   for (int b = 0; b < kLptBuckets; ++b) hist[b][t] = 0;
-  auto bucket = [&](int w) {
-    const int kept = lite_kept(read_list + (long long)w * (nkb + 2), nkb);
-    const int bk = kept * kLptBuckets / (nkb + 1);
-    return bk < kLptBuckets ? bk : kLptBuckets - 1;
-  };
-  for (int w = w0; w < w1; ++w) ++hist[bucket(w)][t];
-  __syncthreads();
-  // Exclusive prefix over (bucket descending, thread ascending).
-  if (t < kLptBuckets) {
-    int sum = 0;
-    for (int u = 0; u < kLptThreads; ++u) {
-      const int c = hist[t][u];
-      hist[t][u] = sum;
-      sum += c;
+  // Bucket of every CTA: rows dealt round robin over the threads, the heads of
+  // 4 rows in flight per thread.
+  for (int wb = t; wb < nctas; wb += 4 * kLptThreads) {
+    int e[4][kLptHead];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int w = wb + u * kLptThreads;
+      if (w < nctas) lite_row_head(read_list + (long long)w * (nkb + 2), nkb, e[u]);
     }
-    bucket_base[t] = sum;  // bucket total, turned into a base below
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int w = wb + u * kLptThreads;
+      if (w < nctas) {
+        const int bk = lite_kept(read_list + (long long)w * (nkb + 2), nkb, e[u]) * kLptBuckets / (nkb + 1);
+        bk_of[w] = (uint8_t)(bk < kLptBuckets ? bk : kLptBuckets - 1);
+      }
+    }
   }
   __syncthreads();
-  if (t == 0) {
-    int acc = 0;
-    for (int b = kLptBuckets - 1; b >= 0; --b) {
-      const int c = bucket_base[b];
-      bucket_base[b] = acc;
-      acc += c;
-    }
+  for (int w = w0; w < w1; ++w) ++hist[bk_of[w]][t];
+  __syncthreads();
+  // Exclusive prefix of each bucket's counts over the threads: wave v takes
+  // buckets v, v+4, ...; lane l holds threads 4l..4l+3 (one conflict-free
+  // 16-byte LDS access each way).
+  const int wv = t >> 6, ln = t & 63;
+  for (int b = wv; b < kLptBuckets; b += kLptThreads / 64) {
+    int4* cell = reinterpret_cast<int4*>(&hist[b][4 * ln]);
+    const int4 c = *cell;
+    const int s1 = c.x + c.y, s2 = s1 + c.z, s3 = s2 + c.w;
+    const int incl = wave_incl_scan(s3);
+    const int excl = incl - s3;
+    *cell = make_int4(excl, excl + c.x, excl + s1, excl + s2);
+    if (ln == 63) bucket_base[b] = incl;  // bucket total, turned into a base below
+  }
+  __syncthreads();
+  // Bucket bases, heaviest first: exclusive scan of the totals in descending
+  // bucket order (lane l holds bucket 63 - l).
+  if (wv == 0) {
+    const int c = bucket_base[kLptBuckets - 1 - ln];
+    bucket_base[kLptBuckets - 1 - ln] = wave_incl_scan(c) - c;
   }
   __syncthreads();
   for (int w = w0; w < w1; ++w) {
-    const int bk = bucket(w);
+    const int bk = bk_of[w];
     order[bucket_base[bk] + hist[bk][t]] = w;
     ++hist[bk][t];
   }

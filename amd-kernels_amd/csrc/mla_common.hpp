@@ -145,8 +145,8 @@ __device__ int search_chunk(long long sumL, int maxL, int B, int budget, UnitsFn
   return hi;
 }
 
-// Wave64 reductions and inclusive scan on DPP row shifts / broadcasts (no LDS).
-__device__ __forceinline__ int wave_incl_scan(int v);
+// Wave64 reductions on DPP row shifts / broadcasts (no LDS); wave_incl_scan is
+// in mm_common.hpp.
 __device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 __device__ __forceinline__ int wave_max_i(int v) {
   // Invalid DPP sources return `old` = the lane's own value (neutral for max).
@@ -157,15 +157,6 @@ __device__ __forceinline__ int wave_max_i(int v) {
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));
   v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));
   return __builtin_amdgcn_readlane(v, 63);
-}
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
-  return v;
 }
 
 struct Unit {

@@ -111,8 +111,19 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------
-// Cross-lane: combine lane l with lane l^32 (v_permlane32_swap on gfx950).
+// Cross-lane: combine lane l with lane l^32 (v_permlane32_swap on gfx950);
+// inclusive wave64 prefix sum on DPP row shifts / broadcasts (no LDS).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
 __device__ __forceinline__ float xor32_max(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);
   const auto pr = __builtin_amdgcn_permlane32_swap(u, u, false, false);

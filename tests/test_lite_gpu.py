@@ -169,16 +169,35 @@ def test_lite_step_matches_oracle(phase, mode):
     assert any(len(ol.decode(r, nkb, phase)[0]) < nkb for r in rows)
 
 
-def test_lite_lpt_order_matches_oracle():
-    """The planning kernel's CTA permutation (through the C ABI) against the
-    oracle's stable heaviest-first order, on rows of very different weights."""
-    Bq, Hq, Sq, Skv = 1, 6, 1024, 4096
-    nqb, nkb = Sq // 256, Skv // 64
+def _lpt_rows(kind, nrows, nkb):
     rng = np.random.default_rng(5)
-    rows = np.zeros((Bq * Hq * nqb, nkb + 2), np.int16)
-    for i in range(len(rows)):
+    if kind == "mixed":
+        # Written rows of many ranges (up to nkb + 1 entries), plus rows whose
+        # length is negative, odd, or past nkb + 1 (clamped).
+        rows = _random_rows(nrows, nkb, 1, seed=11)
+        rows[0, 0] = -3
+        rows[1, :] = rng.integers(-1, nkb, nkb + 2)
+        rows[1, 0] = nkb + 5
+        rows[2, :8] = (7, 40, 3, 9, 1, 30, 12, 20)
+        rows[3, :] = rng.integers(-1, nkb, nkb + 2)
+        rows[3, 0] = 20
+        return rows
+    rows = np.zeros((nrows, nkb + 2), np.int16)
+    for i in range(nrows):
         kept = int(rng.integers(1, nkb + 1))
         rows[i, :3] = (2, kept - 1, -1)
+    return rows
+
+
+@pytest.mark.parametrize("kind", ["counts", "mixed"])
+def test_lite_lpt_order_matches_oracle(kind):
+    """The planning kernel's CTA permutation (through the C ABI) against the
+    oracle's stable heaviest-first order, on rows of very different weights
+    (one range each, or many ranges and out-of-range lengths)."""
+    Bq, Hq, Sq, Skv = 1, 6, 1024, 4096
+    nqb, nkb = Sq // 256, Skv // 64
+    rows = _lpt_rows(kind, Bq * Hq * nqb, nkb)
+    assert kind == "counts" or max(int(r[0]) for r in rows) > 9
     q, k, v = (randn_bf16((Bq, s, Hq, 128), 50 + i).to(DEV) for i, s in enumerate((Sq, Skv, Skv)))
     vt = torch.empty(_lib.lib.moonmath_attention_vt_bytes(Bq, Hq, Skv) // 2, dtype=torch.bfloat16, device=DEV)
     st = _lib.stream_ptr(DEV)
