@@ -33,8 +33,10 @@ constexpr int kQRegPairs = 14;                 // k-step pairs whose Q lives in 
 constexpr int kQLdsDim0 = kQRegPairs * 32;     // 448
 constexpr int kQLdsRowBytes = (kQK - kQLdsDim0) * 2;  // 256
 
-// Split partial records: one per (b, part, query row): O [512] fp32, then all
-// (m, l) pairs after the last O record. kMaxRecords caps the workspace.
+// Split partial records. Workspace: the O records (one per (b, part): rec_rows
+// rows of 512 fp32, row-major, or in the 128-row kernel's fragment order), then
+// the (m, l) pair of every (b, part, query row), then an 8-byte (parts, first
+// record) entry per request. kMaxRecords caps the O rows of a workspace.
 constexpr size_t kMaxRecords = 65536;
 
 struct Params {
@@ -50,9 +52,18 @@ struct Params {
   int B, H, q_len, S_fixed, parts, ngroups, paged;
   int unit_cap;           // units one round of CTAs over the CUs holds
   int qrows;              // H * q_len
+  int rec_rows;           // O rows per split record: qrows, or a multiple of 32 for the fragment order
+  int rec_frag;           // 1: O records in the 128-row kernel's fragment order
   float score_c;          // scale * kv_scale * log2(e), fp32
   float kv_scale;
 };
+
+// Split workspace regions (see kMaxRecords).
+__device__ __forceinline__ float* ws_rec_o(const Params& p, size_t rec) { return p.ws + rec * p.rec_rows * kLat; }
+__device__ __forceinline__ float* ws_ml(const Params& p) { return p.ws + (size_t)p.B * p.parts * p.rec_rows * kLat; }
+__device__ __forceinline__ int* ws_tbl(const Params& p) {
+  return reinterpret_cast<int*>(ws_ml(p) + (size_t)p.B * p.parts * p.qrows * 2);
+}
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));

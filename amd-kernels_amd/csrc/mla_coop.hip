@@ -518,14 +518,14 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
   if (split) {
     // Unnormalised fp32 O of this part: record rec0 * qrows + row.
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(p.ws + rec0 * p.qrows * kLat, (short)0, p.qrows * kLat * 4, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(ws_rec_o(p, rec0), (short)0, p.qrows * kLat * 4, kRsrcWord3);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const u32x4 v = __builtin_bit_cast(u32x4, oacc[j]);
       __builtin_amdgcn_raw_buffer_store_b128(v, rs, (i * kLat + 128 * wave + 16 * j + 4 * G) * 4, 0, 0);
     }
     if (row_ok && G == 0 && wave == 0) {
-      float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + (rec0 * p.qrows + i) * 2;
+      float* pml = ws_ml(p) + (rec0 * p.qrows + i) * 2;
       pml[0] = row_m;
       pml[1] = L;
     }
@@ -543,7 +543,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
   }
   if (p.parts > 1 && part == 0 && tid == 0) {
     // Per-request (parts, first record) table for the merge kernel.
-    int* tbl = reinterpret_cast<int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
+    int* tbl = ws_tbl(p);
     tbl[2 * b] = un.nparts;
     tbl[2 * b + 1] = un.rec0;
   }

@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   // through the tile loop).
   const int qrow_e = grp * kRowsPerCta + (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31);
   const bool row_ok_e = qrow_e < p.qrows;
-  const size_t rec = ((size_t)un.rec0 + part) * p.qrows + qrow_e;
+  const size_t rec = ((size_t)un.rec0 + part) * p.qrows + qrow_e;  // row-major records (rec_rows == qrows)
   uint16_t* orow = p.o_lat + ((long long)qb * p.qrows + qrow_e) * kLat;
   float* prow = p.ws + rec * kLat;
 
@@ -573,58 +573,41 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
     }
   }
   if (split && row_ok_e && g == 0 && wave == 0) {
-    float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + rec * 2;
+    float* pml = ws_ml(p) + rec * 2;
     pml[0] = M;
     pml[1] = L;
   }
   if (p.parts > 1 && part == 0 && grp == 0 && tid == 0) {
     // Per-request (parts, first record) table for the merge kernel.
-    int* tbl = reinterpret_cast<int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
+    int* tbl = ws_tbl(p);
     tbl[2 * b] = un.nparts;
     tbl[2 * b + 1] = un.rec0;
   }
 }
 
-// Merge: one thread = 4 output dims of one (b, query row).
-// M = max_p m_p, w_p = 2^(m_p - M), out = sum w_p O_p * kv_scale / sum w_p l_p.
-__global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
-  const long long cell = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long per_b = (long long)p.qrows * (kLat / 4);
-  if (cell >= per_b * p.B) return;
-  const int b = (int)(cell / per_b);
-  const int rem = (int)(cell % per_b);
-  const int qrow = rem / (kLat / 4);
-  const int d = (rem % (kLat / 4)) * 4;
-  int qb = b;
-  if (p.rows) {
-    qb = p.rows[b];
-    qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
-  }
-  const float* ml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat;
-  const int* tbl = reinterpret_cast<const int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
-  const int nparts = tbl[2 * b];
-  const int rec0 = tbl[2 * b + 1];
-  if (nparts <= 1) return;  // the decode kernel wrote this request's output
-  // The (m, l) pairs and O slices of up to kBatch parts are loaded together,
-  // so a request of up to kBatch parts costs one round of memory latency after
-  // the table; the arithmetic is max-then-weighted-sum in part order.
+// Merge of one 4-dim slice of one query row over its request's parts:
+// M = max_p m_p, w_p = 2^(m_p - M), out = sum w_p O_p * kv_scale / sum w_p l_p,
+// parts in order. o_at(j) / ml_at(j): part j's 16-byte O slice and (m, l) pair.
+// The (m, l) pairs and O slices of up to kBatch parts are loaded together, so a
+// request of up to kBatch parts costs one round of memory latency.
+template <class OAt, class MlAt>
+__device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_at, MlAt ml_at) {
   constexpr int kBatch = 8;
   float M = -__builtin_inff();
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
   float mb[kBatch], lb[kBatch];
   f32x4 ob[kBatch];
-  // Parts past the request's last are not loaded (for even qrows a workgroup's
-  // 256 cells belong to one request, so the branch is uniform).
+  // Parts past the request's last are not loaded (uniform across the CTA: a
+  // CTA's cells belong to one request).
   auto load_batch = [&](int j0) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       if (j0 + k < nparts) {
-        const size_t rec = ((size_t)rec0 + j0 + k) * p.qrows + qrow;
-        const float2 m_l = *reinterpret_cast<const float2*>(ml + rec * 2);
+        const float2 m_l = *reinterpret_cast<const float2*>(ml_at(j0 + k));
         mb[k] = m_l.x;
         lb[k] = m_l.y;
-        ob[k] = *reinterpret_cast<const f32x4*>(p.ws + rec * kLat + d);
+        ob[k] = *reinterpret_cast<const f32x4*>(o_at(j0 + k));
       } else {
         mb[k] = -__builtin_inff();
         lb[k] = 0.f;
@@ -657,7 +640,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
 #pragma unroll
       for (int k = 0; k < kBatch; ++k) {
         const int j = j0 + k < nparts ? j0 + k : nparts - 1;
-        M = fmaxf(M, ml[(((size_t)rec0 + j) * p.qrows + qrow) * 2]);
+        M = fmaxf(M, ml_at(j)[0]);
       }
     }
     for (int j0 = 0; j0 < nparts; j0 += kBatch) {
@@ -665,11 +648,80 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
       accumulate(j0);
     }
   }
-  const float inv = (L == 0.f) ? 0.f : p.kv_scale * __builtin_amdgcn_rcpf(L);
+  const float inv = (L == 0.f) ? 0.f : kv_scale * __builtin_amdgcn_rcpf(L);
   u32x2 o;
   o[0] = pack2_bf16_canon<kRTNE>(acc[0] * inv, acc[1] * inv);
   o[1] = pack2_bf16_canon<kRTNE>(acc[2] * inv, acc[3] * inv);
+  return o;
+}
+
+__device__ __forceinline__ int merge_out_row(const Params& p, int b) {
+  int qb = b;
+  if (p.rows) {
+    qb = p.rows[b];
+    qb = qb < 0 ? 0 : (qb >= p.B ? p.B - 1 : qb);
+  }
+  return qb;
+}
+
+// Merge of row-major records: one thread = 4 output dims of one (b, query row).
+__global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
+  const long long cell = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long per_b = (long long)p.qrows * (kLat / 4);
+  if (cell >= per_b * p.B) return;
+  const int b = (int)(cell / per_b);
+  const int rem = (int)(cell % per_b);
+  const int qrow = rem / (kLat / 4);
+  const int d = (rem % (kLat / 4)) * 4;
+  const int qb = merge_out_row(p, b);
+  const float* ml = ws_ml(p);
+  const int* tbl = ws_tbl(p);
+  const int nparts = tbl[2 * b];
+  const int rec0 = tbl[2 * b + 1];
+  if (nparts <= 1) return;  // the decode kernel wrote this request's output
+  const u32x2 o = merge_slice(
+      nparts, p.kv_scale, [&](int j) { return ws_rec_o(p, (size_t)rec0 + j) + (size_t)qrow * kLat + d; },
+      [&](int j) { return ml + (((size_t)rec0 + j) * p.qrows + qrow) * 2; });
   *reinterpret_cast<u32x2*>(p.o_lat + ((long long)qb * p.qrows + qrow) * kLat + d) = o;
+}
+
+// Merge of the 128-row kernel's fragment-order records (see its epilogue):
+// CTA (b, wave slice w, row tile rt) reads the 16 KB of its 32 rows x 128 dims
+// from each part, 16 contiguous bytes per thread, and writes the rows' 256-byte
+// output spans through LDS.
+constexpr int kMergeFragThreads = 1024;
+__global__ __launch_bounds__(kMergeFragThreads) void mla_merge_frag_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[32][128];
+  const int nrt = p.rec_rows / 32;
+  const int b = blockIdx.x / (4 * nrt);
+  const int k = blockIdx.x % (4 * nrt);  // w * nrt + rt
+  const int w = k / nrt, rt = k % nrt;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, i4 = (tid >> 6) & 3, j = tid >> 8;
+  const int n = lane & 31, g = lane >> 5;
+  const int* tbl = ws_tbl(p);
+  const int nparts = tbl[2 * b];
+  const int rec0 = tbl[2 * b + 1];
+  if (nparts <= 1) return;  // uniform: the decode kernel wrote this request's output
+  const int row = 32 * rt + n;
+  const int mrow = row < p.qrows ? row : p.qrows - 1;  // padding rows read a valid (m, l)
+  const size_t f = ((size_t)(k * 4 + j) * 4 + i4) * 64 + lane;  // 16-byte unit in the record
+  const float* ml = ws_ml(p);
+  const u32x2 o = merge_slice(
+      nparts, p.kv_scale, [&](int jj) { return ws_rec_o(p, (size_t)rec0 + jj) + f * 4; },
+      [&](int jj) { return ml + (((size_t)rec0 + jj) * p.qrows + mrow) * 2; });
+  *reinterpret_cast<u32x2*>(&tile[n][32 * j + 8 * i4 + 4 * g]) = o;
+  __syncthreads();
+  // 32 rows x 256 B: thread t < 512 stores 16 B of row t / 16.
+  if (tid < 512) {
+    const int r = tid >> 4, c = tid & 15;
+    const int orow = 32 * rt + r;
+    if (orow < p.qrows) {
+      const int qb = merge_out_row(p, b);
+      *reinterpret_cast<u32x4*>(p.o_lat + ((long long)qb * p.qrows + orow) * kLat + 128 * w + 8 * c) =
+          *reinterpret_cast<const u32x4*>(&tile[r][8 * c]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -750,9 +802,22 @@ int ngroups_for(int H, int q_len) {
   return (H * q_len + rows - 1) / rows;
 }
 
+// O rows of one split record: the 128-row kernel writes whole 32-row tiles in
+// its fragment order; the others write qrows row-major rows.
+int rec_rows_for(int H, int q_len) {
+  const int qrows = H * q_len;
+  return use_wide(H, q_len) ? 32 * ((qrows + 31) / 32) : qrows;
+}
+
+// Split workspace bytes: O records, (m, l) pairs, the per-request table.
+size_t split_ws_bytes(int B, int H, int parts, int q_len) {
+  return (size_t)B * parts * ((size_t)rec_rows_for(H, q_len) * kLat + (size_t)H * q_len * 2) * sizeof(float) +
+         (size_t)B * 8;
+}
+
 // Largest parts the fixed record workspace allows for (B, H, q_len).
 int max_parts_for(int B, int H, int q_len) {
-  const long long per_part = (long long)B * H * q_len;
+  const long long per_part = (long long)B * rec_rows_for(H, q_len);
   long long m = per_part > 0 ? (long long)kMaxRecords / per_part : 1;
   if (m > kMaxParts) m = kMaxParts;
   return m < 1 ? 1 : (int)m;
@@ -822,6 +887,8 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   p.unit_cap = unit_cap_for(H, q_len);
   p.paged = paged ? 1 : 0;
   p.qrows = H * q_len;
+  p.rec_rows = rec_rows_for(H, q_len);
+  p.rec_frag = use_wide(H, q_len) ? 1 : 0;
   p.score_c = (float)((double)scale * (double)kv_scale * 1.4426950408889634);
   p.kv_scale = kv_scale;
   // Unit slots per XCD for the snake deal of units 0..U-1, U <= B * parts (the
@@ -839,7 +906,10 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
     hipLaunchKernelGGL(mla_decode_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
-  if (p.parts > 1) {
+  if (p.parts > 1 && p.rec_frag) {
+    const long long ctas = (long long)B * 4 * (p.rec_rows / 32);
+    hipLaunchKernelGGL(mla_merge_frag_kernel, dim3((unsigned)ctas), dim3(kMergeFragThreads), 0, st, p);
+  } else if (p.parts > 1) {
     const long long cells = (long long)B * p.qrows * (kLat / 4);
     hipLaunchKernelGGL(mla_merge_kernel, dim3((unsigned)((cells + 255) / 256)), dim3(256), 0, st, p);
   }
@@ -857,7 +927,7 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
 // entry the merge reads, so nothing needs clearing between calls; calls that
 // overlap on one GPU share the array and race.
 // ---------------------------------------------------------------------------
-constexpr size_t kScratchRecords = 32768;  // B * parts * H * q_len at most
+constexpr size_t kScratchRecords = 32768;  // B * parts * rec_rows_for(H, q_len) at most
 constexpr size_t kScratchBytes = kScratchRecords * (kLat + 2) * sizeof(float) + (size_t)kMaxPagedB * 8;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -891,8 +961,7 @@ size_t mla_decode_a16w8_workspace_bytes(void) { return kMaxRecords * (kLat + 2) 
 
 size_t mla_decode_a16w8_multiq_workspace_for(int B, int H, int parts, int q_len) {
   if (B < 1 || H < 1 || q_len < 1) return 0;
-  const int p = clamp_parts(parts, B, H, q_len, true);
-  return (size_t)B * p * H * q_len * (kLat + 2) * sizeof(float) + (size_t)B * 8;
+  return split_ws_bytes(B, H, clamp_parts(parts, B, H, q_len, true), q_len);
 }
 
 int launch_mla_decode_a16w8(const void* q_lat, const void* q_pe, const void* c_kv, const void* k_pe, void* o_lat,
@@ -927,7 +996,7 @@ int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_p
   const int eff = clamp_parts(parts, B, H, q_len, true);
   void* ws = nullptr;
   if (eff > 1) {
-    if ((size_t)B * eff * H * q_len > kScratchRecords) return -9;
+    if ((size_t)B * eff * rec_rows_for(H, q_len) > kScratchRecords) return -9;
     const int rc = scratch_ptr(&ws);
     if (rc != 0) return rc;
   }

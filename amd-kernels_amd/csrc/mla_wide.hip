@@ -584,22 +584,29 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer access, gfx9 family
   const int row0 = rb * kWRows + n;       // this lane's row in row tile 0
   if (split) {
-    // Unnormalised fp32 O of this part: record rec0 * qrows + row.
+    // Unnormalised fp32 O of this part, record rec0 in fragment order: the
+    // 16 bytes of (wave, row tile rt < rec_rows / 32, d-tile j, i4, lane) at
+    // 16 * ((((wave * nrt + rt) * 4 + j) * 4 + i4) * 64 + lane), so every
+    // store instruction writes 1 KB contiguous (row-major stores from this
+    // register layout write 16 B per 2 KB row: ~3x slower at 256 KB per CTA).
+    const int nrt = p.rec_rows / 32;
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(p.ws + rec0 * p.qrows * kLat, (short)0, p.qrows * kLat * 4, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(ws_rec_o(p, rec0), (short)0, p.rec_rows * kLat * 4, kRsrcWord3);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
+      if (rt < nrt) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          // Whole-vector bit cast: a bit cast of a single vector element
-          // reinterprets element 0 with this compiler.
-          const f32x4 f = {oacc[4 * j + rt][4 * i4], oacc[4 * j + rt][4 * i4 + 1], oacc[4 * j + rt][4 * i4 + 2],
-                           oacc[4 * j + rt][4 * i4 + 3]};
-          const u32x4 v = __builtin_bit_cast(u32x4, f);
-          const int off = ((row0 + 32 * rt) * kLat + 32 * (4 * wave + j) + 8 * i4 + 4 * g) * 4;
-          __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+          for (int i4 = 0; i4 < 4; ++i4) {
+            // Whole-vector bit cast: a bit cast of a single vector element
+            // reinterprets element 0 with this compiler.
+            const f32x4 f = {oacc[4 * j + rt][4 * i4], oacc[4 * j + rt][4 * i4 + 1], oacc[4 * j + rt][4 * i4 + 2],
+                             oacc[4 * j + rt][4 * i4 + 3]};
+            const u32x4 v = __builtin_bit_cast(u32x4, f);
+            const int off = ((((wave * nrt + rt) * 4 + j) * 4 + i4) * 64 + lane) * 16;
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+          }
         }
       }
     }
@@ -624,13 +631,13 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
     }
   }
   if (split && row_ok && g == 0) {
-    float* pml = p.ws + (size_t)p.B * p.parts * p.qrows * kLat + (rec0 * p.qrows + qrow) * 2;
+    float* pml = ws_ml(p) + (rec0 * p.qrows + qrow) * 2;
     pml[0] = row_m;
     pml[1] = mlb[2 * (32 * wave + n) + 1];
   }
   if (p.parts > 1 && part == 0 && rb == 0 && tid == 0) {
     // Per-request (parts, first record) table for the merge kernel.
-    int* tbl = reinterpret_cast<int*>(p.ws + (size_t)p.B * p.parts * p.qrows * (kLat + 2));
+    int* tbl = ws_tbl(p);
     tbl[2 * b] = un.nparts;
     tbl[2 * b + 1] = un.rec0;
   }

@@ -143,8 +143,9 @@ int launch_mla_decode_a16w8_paged_dev(const void* q_lat, const void* q_pe, const
  * HIP graph capture, serving loops that forbid hipMalloc). The split records
  * live in a 64.3 MiB device array of the library (held on each GPU the library
  * runs on until the process ends); the call performs no allocation. Limit:
- * B * parts * H * q_len <= 32768 split records once parts is clamped as in
- * the workspace launcher (parts 1 needs none), else returns -9 with nothing
+ * B * parts * R <= 32768 split-record rows once parts is clamped as in the
+ * workspace launcher (parts 1 needs none), R = H * q_len, rounded up to a
+ * multiple of 32 when 96 <= H * q_len <= 128; else returns -9 with nothing
  * launched. Calls that overlap on one GPU share the array and race: serialise
  * them (one stream, or events). */
 int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_pe, const void* kv_pool, void* o_lat,

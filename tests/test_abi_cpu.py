@@ -93,12 +93,17 @@ def test_mla_launcher_argument_codes():
 
 
 def test_mla_planners():
-    for B, H, S, ql in [(64, 128, 8192, 1), (64, 128, 8192, 2), (64, 16, 8192, 1), (2, 16, 2048, 4), (1, 1, 1, 1)]:
+    for B, H, S, ql in [(64, 128, 8192, 1), (64, 128, 8192, 2), (64, 16, 8192, 1), (2, 16, 2048, 4), (1, 1, 1, 1),
+                        (8, 100, 4096, 1), (8, 48, 4096, 2)]:
         p = ma.mla_decode_a16w8_plan_parts_q(B, S, ql, H)
         assert 1 <= p <= max(1, -(-S // 32))
         eff = _lib.lib.moonmath_mla_effective_parts(B, H, p, ql, 1)
         assert eff == p  # planned parts always fit the workspace
-        assert _lib.lib.mla_decode_a16w8_multiq_workspace_for(B, H, p, ql) == B * p * H * ql * 514 * 4 + 8 * B
+        # O records of R rows (the 128-row kernel's whole 32-row tiles for 96..128
+        # query rows), an (m, l) pair per query row and part, 8 bytes per request.
+        qrows = H * ql
+        R = 32 * -(-qrows // 32) if 96 <= qrows <= 128 else qrows
+        assert _lib.lib.mla_decode_a16w8_multiq_workspace_for(B, H, p, ql) == B * p * (R * 512 + qrows * 2) * 4 + 8 * B
     assert _lib.lib.moonmath_mla_effective_parts(4, 16, 9, 1, 0) == 1  # no workspace -> no split
 
 
