@@ -123,16 +123,20 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   // in-order vmcnt), while Q, the table build and the first tiles' gathers
   // overlap. Staging layout: see the table build in sweep().
   char* stg = ring + wave * (kWStageTiles * 128);
+  // Tile pairs this wave stages in the round of 256 tiles from r0: pairs
+  // wave, wave + 4, ... (pair q of the wave = tiles r0 + 8q + 2 wave + {0, 1}).
+  auto stage_pairs = [&](int ntiles, int r0) {
+    const int np = (ntiles - r0 - 2 * wave + 7) / 8;
+    return np < 0 ? 0 : (np > kWStageTiles / 2 ? kWStageTiles / 2 : np);
+  };
   auto stage_round = [&](int seg_lo, int seg_hi, int ntiles, int r0) {
-    const int j0 = r0 + kWStageTiles * wave;
-    int nb = ntiles - j0;
-    nb = nb < 0 ? 0 : (nb > kWStageTiles ? kWStageTiles : nb);
-    for (int q = 0; q < (nb + 1) / 2; ++q) {
-      int tok = seg_lo + kTileTok * (j0 + 2 * q + g) + n;
+    const int np = stage_pairs(ntiles, r0);
+    for (int q = 0; q < np; ++q) {
+      int tok = seg_lo + kTileTok * (r0 + 8 * q + 2 * wave + g) + n;
       tok = tok < seg_hi ? tok : seg_hi - 1;
       dma4_opaque(p.kv_indices + slot0 + tok, stg + 256 * q);
     }
-    return nb;
+    return np;
   };
   auto seg_end = [&](int seg_lo) {
     return (long long)seg_lo + kWTabTiles * kTileTok < kv_hi ? seg_lo + kWTabTiles * kTileTok : kv_hi;
@@ -220,26 +224,24 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
       if constexpr (PAGED) {
         // Tile table: tab[j] = slot of tile j's first token when its valid
         // tokens occupy consecutive slots (one base + lane offsets), else -1.
-        // Wave w stages the slot indices of tiles 64w .. 64w+63 of each round
-        // of 256 in its own 8 KB of the ring (two tiles per 4-byte DMA).
+        // Each wave stages the slot indices of every fourth tile pair of a
+        // round of 256 tiles in its own 8 KB of the ring (two tiles per 4-byte
+        // DMA) and builds their entries, so the 4 waves share the build.
         for (int r0 = 0; r0 < ntiles; r0 += kWWaves * kWStageTiles) {
-          int nb;
+          int np;
           if (prestaged) {
             // First round of the first segment, staged before the Q loads:
             // wait for it only.
-            const int j0 = kWStageTiles * wave;
-            nb = ntiles - j0;
-            nb = nb < 0 ? 0 : (nb > kWStageTiles ? kWStageTiles : nb);
+            np = stage_pairs(ntiles, 0);
             static_assert(kQLoads == 36, "the vmcnt below counts the Q loads");
             asm volatile("s_waitcnt vmcnt(36)" ::: "memory");
             prestaged = false;
           } else {
-            nb = stage_round(seg_lo, seg_hi, ntiles, r0);
+            np = stage_round(seg_lo, seg_hi, ntiles, r0);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
           }
-          const int j0 = r0 + kWStageTiles * wave;
-          for (int q = 0; q < (nb + 1) / 2; ++q) {
-            const int j = j0 + 2 * q + g;
+          for (int q = 0; q < np; ++q) {
+            const int j = r0 + 8 * q + 2 * wave + g;
             const int v = *reinterpret_cast<const int*>(stg + 256 * q + 4 * lane);
             const int f0 = __builtin_amdgcn_readlane(v, 0), f1 = __builtin_amdgcn_readlane(v, 32);
             const int first = g ? f1 : f0;
