@@ -787,8 +787,9 @@ constexpr int kMaxParts = 64;
 // (steady clocks): H=128 q_len 1: 108 us wide (4 parts) vs 131 us 32-row
 // unsplit, 120-124 us 32-row with 2 parts (two rounds of CTAs, in request or
 // longest-first order) and 149-153 us with 4 parts; H=128 q_len 2 (two row
-// blocks): 213 us wide vs 185 us 32-row -- with several row blocks the split
-// records (rows x parts x 2 KB) outweigh the shared tile loads.
+// blocks, one round of 256 CTAs with 2 parts, fragment-order records): 187 us
+// wide vs 180-182 us 32-row -- with several row blocks the split records
+// (rows x parts x 2 KB) outweigh the shared tile loads.
 constexpr int kWideMinRows = 96;
 constexpr int kWideRowsPerCta = 128;
 // Requests of at most 16 query rows run mla_coop_kernel (the 4 waves share each

@@ -587,16 +587,17 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
   const int row0 = rb * kWRows + n;       // this lane's row in row tile 0
   if (split) {
     // Unnormalised fp32 O of this part, record rec0 in fragment order: the
-    // 16 bytes of (wave, row tile rt < rec_rows / 32, d-tile j, i4, lane) at
-    // 16 * ((((wave * nrt + rt) * 4 + j) * 4 + i4) * 64 + lane), so every
-    // store instruction writes 1 KB contiguous (row-major stores from this
-    // register layout write 16 B per 2 KB row: ~3x slower at 256 KB per CTA).
+    // 16 bytes of (wave, row tile RT = 4 rb + rt < rec_rows / 32, d-tile j,
+    // i4, lane) at 16 * ((((wave * nrt + RT) * 4 + j) * 4 + i4) * 64 + lane),
+    // so every store instruction writes 1 KB contiguous (row-major stores from
+    // this register layout write 16 B per 2 KB row: ~3x slower at 256 KB per
+    // CTA).
     const int nrt = p.rec_rows / 32;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(ws_rec_o(p, rec0), (short)0, p.rec_rows * kLat * 4, kRsrcWord3);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      if (rt < nrt) {
+      if (4 * rb + rt < nrt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -606,7 +607,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
             const f32x4 f = {oacc[4 * j + rt][4 * i4], oacc[4 * j + rt][4 * i4 + 1], oacc[4 * j + rt][4 * i4 + 2],
                              oacc[4 * j + rt][4 * i4 + 3]};
             const u32x4 v = __builtin_bit_cast(u32x4, f);
-            const int off = ((((wave * nrt + rt) * 4 + j) * 4 + i4) * 64 + lane) * 16;
+            const int off = ((((wave * nrt + 4 * rb + rt) * 4 + j) * 4 + i4) * 64 + lane) * 16;
             __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
           }
         }
