@@ -326,21 +326,28 @@ def test_max_fallback_on_growing_scores(H, q_len, S, paged, parts):
     print(_check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy()))
 
 
-def test_paged_rows_remaps_query_and_output():
-    """Reference tests/test_mla_decode.py:164-188: reversing rows reverses the batch."""
-    B, H, q_len = 4, 16, 4
+@pytest.mark.parametrize("H,q_len", [(16, 4), (16, 1), (128, 1), (100, 1)])
+def test_paged_rows_remaps_query_and_output(H, q_len):
+    """Reference tests/test_mla_decode.py:164-188: reversing rows reverses the
+    batch; on the 32-row, 16-row and 128-row kernels (each split, so the row
+    map also reaches both merge kernels; H=100 leaves padding rows in the
+    128-row kernel's records)."""
+    B = 4
     lens = [2048] * B
     pool, idx, indptr = paged_pool(lens, 57)
     q_lat, q_pe = rand_q(B, q_len, H, 57)
+    if q_len == 1:
+        q_lat, q_pe = q_lat[:, 0].contiguous(), q_pe[:, 0].contiguous()
     lens_t = _d(torch.tensor(lens, dtype=torch.int32))
-    parts = ma.mla_decode_a16w8_multiq_plan_parts_q(B, lens[0], q_len, H)
-    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
-    ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, lens_t, None, _d(idx), _d(indptr),
-                                         parts, SCALE_576, KV_SCALE)
+    parts = ma.mla_decode_a16w8_plan_parts_q(B, lens[0], q_len, H)
+    assert parts > 1
+    o = torch.zeros(*q_lat.shape[:-1], 512, dtype=torch.bfloat16, device=DEV)
+    ma.mla_decode_a16w8_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, lens_t, None, _d(idx), _d(indptr),
+                                  parts, SCALE_576, KV_SCALE)
     rows = _d(torch.arange(B - 1, -1, -1, dtype=torch.int32))
     o_rev = torch.zeros_like(o)
-    ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat.flip(0).contiguous()), _d(q_pe.flip(0).contiguous()), _d(pool),
-                                         o_rev, lens_t, rows, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
+    ma.mla_decode_a16w8_paged_dev(_d(q_lat.flip(0).contiguous()), _d(q_pe.flip(0).contiguous()), _d(pool),
+                                  o_rev, lens_t, rows, _d(idx), _d(indptr), parts, SCALE_576, KV_SCALE)
     torch.cuda.synchronize()
     assert torch.equal(o_rev.flip(0).view(torch.int16), o.view(torch.int16))
 
