@@ -424,11 +424,13 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       const char* kst3 = kring + ((i + 3) % kRing) * kKBytes;
       const char* vst3 = vring + ((i + 3) % kRing) * kVBytes;
       auto dma3_step = [&](int d) {  // d = 0, 1: K instructions; 2, 3: V instructions
-        const char* src = d < 2 ? kbase3 + koff[d] : vbase3 + voff + (d - 2) * kFragBytes;
+        // Global address = SGPR base + 32-bit lane offset (no 64-bit VALU add).
+        const char* base = d < 2 ? kbase3 : vbase3;
+        const uint32_t off = d < 2 ? koff[d] : voff + (uint32_t)((d - 2) * kFragBytes);
         const char* dst = d < 2 ? kst3 + (wave * 2 + d) * kFragBytes : vst3 + (wave * 2 + d - 2) * kFragBytes;
         const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)dst;
-        asm volatile("s_cmp_eq_u32 %2, 0\n\ts_cbranch_scc1 1f\n\tglobal_load_lds_dwordx4 %0, off\n1:" ::"v"(src),
-                     "{m0}"(m0v), "s"(pd3)
+        asm volatile("s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\tglobal_load_lds_dwordx4 %0, %1\n1:" ::"v"(off),
+                     "s"(base), "{m0}"(m0v), "s"(pd3)
                      : "memory", "scc");
       };
       mask(scur, kb);
