@@ -208,20 +208,27 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   const int kv_end = p.Skv < kb_end * kKvBlock ? p.Skv : kb_end * kKvBlock;
 
   // LDS: K ring [kRing] | V_t ring [kRing].
-  // K slot: row-major [64 rows][256 B], the 16-byte chunk c of row k stored at
-  // chunk position c ^ (k & 15): one DMA instruction moves 4 whole rows
-  // (coalesced 256-byte reads) and the MFMA fragment reads are conflict free.
+  // K slot: 4 groups of 16 rows, chunk-major inside a group: the 16-byte chunk
+  // c of row k at byte (k / 16) * 4096 + c * 256 + (k % 16) * 16. One DMA
+  // instruction (1 KB) moves chunks 4j..4j+3 of 16 rows (64 contiguous bytes
+  // per row); an MFMA fragment read (chunk 2ds+g of 32 rows) touches 16
+  // consecutive 16-byte cells per 16 lanes (conflict free), and the 8 reads of
+  // a row tile differ only by the immediate offset 512 * ds.
   // V_t slot: fragments [t(2)][s(2)][dt(4)], 1 KB each in lane order.
   char* kring = lds;
   char* vring = lds + kRing * kKBytes;
-  // Lane byte offsets of this wave's 2 K-DMA instructions within a block (16
-  // instructions of 4 rows each per block, 2 per wave).
+  auto kslot_off = [](int k, int c) { return (k >> 4) * 4096 + c * 256 + (k & 15) * 16; };
+  // This lane's MFMA fragment cell for row tile t, k-step ds: kfrag_lane +
+  // 8192 t + 512 ds (rows t*32 + r, chunk 2 ds + g), constants the LDS reads
+  // carry as immediate offsets.
+  const int kfrag_lane = kslot_off(r, g);
+  // Lane source row / chunk of this wave's 2 K-DMA instructions (instruction
+  // j = 2 wave + i fills slot bytes 1024 j .. 1024 j + 1023).
+  auto kdma_row = [&](int i) { return 16 * ((wave * 2 + i) >> 2) + (lane & 15); };
+  auto kdma_chunk = [&](int i) { return 4 * ((wave * 2 + i) & 3) + (lane >> 4); };
   uint32_t koff[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = (wave * 2 + i) * 4 + (lane >> 4);
-    koff[i] = (uint32_t)(row * row_stride * 2) + (uint32_t)((((lane & 15) ^ (row & 15))) * 16);
-  }
+  for (int i = 0; i < 2; ++i) koff[i] = (uint32_t)(kdma_row(i) * row_stride * 2) + (uint32_t)(kdma_chunk(i) * 16);
   const long long kblk_bytes = (long long)kKvBlock * row_stride * 2;
   auto issue_k = [&](int kb, int slot) {
     char* st = kring + slot * kKBytes;
@@ -233,11 +240,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // Last partial block: clamp rows past Skv (they are masked in softmax).
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int row = (wave * 2 + i) * 4 + (lane >> 4);
-        int kv = kb * kKvBlock + row;
+        int kv = kb * kKvBlock + kdma_row(i);
         kv = kv < p.Skv ? kv : p.Skv - 1;
-        dma16(kh + (long long)kv * row_stride * 2 + (((lane & 15) ^ (row & 15)) * 16),
-              (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
+        dma16(kh + (long long)kv * row_stride * 2 + kdma_chunk(i) * 16, (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
       }
     }
   };
@@ -330,9 +335,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int row = t * 32 + r;
-        const bf16x8 kf =
-            *reinterpret_cast<const bf16x8*>(kst + row * 256 + (((2 * ds + g) ^ (row & 15)) << 4));
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + kfrag_lane + 8192 * t + 512 * ds);
         s[t] = mfma32(kf, qf[ds], s[t]);
       }
     }
@@ -489,8 +492,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         }
       };
       auto kfrag = [&](int t, int ds) {
-        const int row = t * 32 + r;
-        return *reinterpret_cast<const bf16x8*>(kst + row * 256 + (((2 * ds + g) ^ (row & 15)) << 4));
+        return *reinterpret_cast<const bf16x8*>(kst + kfrag_lane + 8192 * t + 512 * ds);
       };
       // V^T fragments in a 4-deep rolling buffer, 4 MFMAs ahead: PV MFMA n (0..15)
       // = row tile n/8, k-step (n/4)%2, d-tile n%4.
