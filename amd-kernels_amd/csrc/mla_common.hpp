@@ -32,6 +32,14 @@ constexpr float kGrowLimit = 64.f;
 constexpr int kQRegPairs = 14;                 // k-step pairs whose Q lives in VGPRs
 constexpr int kQLdsDim0 = kQRegPairs * 32;     // 448
 constexpr int kQLdsRowBytes = (kQK - kQLdsDim0) * 2;  // 256
+// Order of the k-step pairs in the QK loops: position s handles pair
+// qk_pair_at(s). The four LDS-resident pairs run at positions 6..9, not last,
+// so their one-step-ahead Q reads overlap the K reads already in flight (and,
+// in the 128-row kernel, steps that also carry PV MFMAs): -2% for the 32-row
+// kernel at H=128 q_len 2. The scores are fp32 sums in a different order,
+// equally close to the exact sum.
+__device__ __forceinline__ constexpr int qk_pair_at(int s) { return s < 6 ? s : (s < 10 ? s + 8 : s - 4); }
+static_assert(kQRegPairs == 14 && kKPairs == 18, "qk_pair_at permutes 18 pairs with the LDS ones at 6..9");
 
 // Split partial records. Workspace: the O records (one per (b, part): rec_rows
 // rows of 512 fp32, row-major, or in the 128-row kernel's fragment order), then

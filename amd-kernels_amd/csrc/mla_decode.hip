@@ -346,7 +346,7 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
       auto qk = [&](auto with_dma) {
         u32x4 kraw[kKAhead];
 #pragma unroll
-        for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(s));
+        for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(qk_pair_at(s)));
         bf16x8 qpa, qpb;  // LDS-resident Q of the next pair, read one step ahead
         f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
@@ -354,18 +354,21 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
           if constexpr (decltype(with_dma)::value)
             dma16_sbase(nbase + (s / 9) * 16 * kQK, dma_offv(s % 9), nst + 1024 * s);
           const u32x4 raw = kraw[s % kKAhead];
-          if (s + kKAhead < kKPairs) kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(s + kKAhead));
+          if (s + kKAhead < kKPairs)
+            kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(qk_pair_at(s + kKAhead)));
+          const int pp = qk_pair_at(s);
           bf16x8 qa, qb2;
-          if (s >= kQRegPairs) {
+          if (pp >= kQRegPairs) {
             qa = qpa;
             qb2 = qpb;
           } else {
-            qa = qf[2 * s];
-            qb2 = qf[2 * s + 1];
+            qa = qf[2 * pp];
+            qb2 = qf[2 * pp + 1];
           }
-          if (s + 1 >= kQRegPairs && s + 1 < kKPairs) {
+          const int pn = s + 1 < kKPairs ? qk_pair_at(s + 1) : 0;
+          if (pn >= kQRegPairs) {
             const char* qrow_p = qpe_lds + n * kQLdsRowBytes;
-            const int c0 = 4 * (s + 1 - kQRegPairs) + 2 * g;  // chunk of dims 32(s+1) + 16g
+            const int c0 = 4 * (pn - kQRegPairs) + 2 * g;  // chunk of dims 32 pn + 16g
             qpa = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * (c0 ^ (n & 15)));
             qpb = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * ((c0 + 1) ^ (n & 15)));
           }

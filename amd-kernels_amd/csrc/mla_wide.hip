@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
         auto paddr = [&](int kk, int rt) { return reinterpret_cast<const bf16x8*>(pr + (2 * rt + kk) * 1024); };
         u32x4 kraw[kKAhead];
 #pragma unroll
-        for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(s));
+        for (int s = 0; s < kKAhead; ++s) kraw[s] = *reinterpret_cast<const u32x4*>(kaddr(qk_pair_at(s)));
         bf16x8 pop[4];  // P^T operand of each row tile (k-step 0, then reloaded for k-step 1)
         i32x2 vraw[4];  // V^T fragment of each d-tile (k-step 0, then reloaded for k-step 1)
         bf16x8 va;
@@ -380,18 +380,21 @@ __global__ __launch_bounds__(kWThreads, 1) void mla_wide_kernel(Params p) {
           if (s < 4) dma_if(pending, s);
           if (s == 4) dma_if(pending && five, 4);
           const u32x4 raw = kraw[s % kKAhead];
-          if (s + kKAhead < kKPairs) kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(s + kKAhead));
+          if (s + kKAhead < kKPairs)
+            kraw[s % kKAhead] = *reinterpret_cast<const u32x4*>(kaddr(qk_pair_at(s + kKAhead)));
+          const int pp = qk_pair_at(s);
           bf16x8 qa, qb2;
-          if (s >= kQRegPairs) {
+          if (pp >= kQRegPairs) {
             qa = qpa;
             qb2 = qpb;
           } else {
-            qa = qf[2 * s];
-            qb2 = qf[2 * s + 1];
+            qa = qf[2 * pp];
+            qb2 = qf[2 * pp + 1];
           }
-          if (s + 1 >= kQRegPairs && s + 1 < kKPairs) {
+          const int pn = s + 1 < kKPairs ? qk_pair_at(s + 1) : 0;
+          if (pn >= kQRegPairs) {
             const char* qrow_p = qlds + n * kQLdsRowBytes;
-            const int c0 = 4 * (s + 1 - kQRegPairs) + 2 * g;  // chunk of dims 32(s+1) + 16g
+            const int c0 = 4 * (pn - kQRegPairs) + 2 * g;  // chunk of dims 32 pn + 16g
             qpa = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * (c0 ^ (n & 15)));
             qpb = *reinterpret_cast<const bf16x8*>(qrow_p + 16 * ((c0 + 1) ^ (n & 15)));
           }
