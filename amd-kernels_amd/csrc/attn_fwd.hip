@@ -373,6 +373,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
 
   f32x16 sA[2], sB[2];
   bf16x8 pf[2][2];
+  // Operands of the last 4 PV MFMAs of the previous block (row tile 1, k-step
+  // 1: V^T fragments 12..15 and P^T), which run after the next block barrier.
+  // Zero before the first block, so those MFMAs then add exact zeros.
+  bf16x8 vtail[4] = {};
+  bf16x8 ptail = {};
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
@@ -439,8 +444,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       mask(scur, kb);
       // Sliced pipeline: QK(i+1) (16 MFMAs) carries softmax(i) of row tile 0
       // and the first half of row tile 1; PV(i) of row tile 0 (8 MFMAs) carries
-      // the rest; PV(i) of row tile 1 follows. Per-accumulator orders (S, O and
-      // each lpart sum) are those of an unsliced softmax.
+      // the rest; PV(i) of row tile 1 follows, its second k-step after the next
+      // barrier. Per-accumulator orders (S, O and each lpart sum) are those of
+      // an unsliced softmax.
       const char* kst = kring + ((i + 1) % kRing) * kKBytes;  // last block: stale slot, unused
       const char* vst = vring + (i % kRing) * kVBytes;
       const float neg_m0 = -row_m;
@@ -506,6 +512,14 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       snext[0] = f32x16{};
       snext[1] = f32x16{};
       bf16x8 kf0 = kfrag(0, 0), kf1 = kfrag(1, 0);
+      // The previous block's last 4 PV MFMAs (operands in registers since
+      // before the barrier) cover the latency of these first K reads:
+      // 1.435 -> 1.411 ms at the headline shape (RTNA, one box).
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
+        sched_fence();
+      }
       bf16x8 vb[4];
 #pragma unroll
       for (int ds = 0; ds < 8; ++ds) {
@@ -550,21 +564,26 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
       pack_pf(1);
-      // PV of row tile 1; lite: with the block max of the vote (4 scores per MFMA).
+      // PV of row tile 1, k-step 0 (k-step 1 runs after the next barrier, from
+      // vtail / ptail); lite: with the block max of the vote (8 scores per MFMA).
       float vmx = -__builtin_inff();
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const int ss = m >> 2, dt = m & 3;
-        const bf16x8 a = vb[m & 3];
-        if (m + 4 < 8) vb[m & 3] = vfrag_n(8 + m + 4);
-        oacc[dt] = mfma32(a, pf[1][ss], oacc[dt]);
+      for (int m = 0; m < 4; ++m) {
+        const bf16x8 a = vb[m];
+        vb[m] = vfrag_n(12 + m);
+        oacc[m] = mfma32(a, pf[1][0], oacc[m]);
         if constexpr (LITE) {
-          const int e0 = 4 * (m & 3);
-          vmx = fmaxf(fmaxf(vmx, scur[m >> 2][e0]), scur[m >> 2][e0 + 1]);
-          vmx = fmaxf(fmaxf(vmx, scur[m >> 2][e0 + 2]), scur[m >> 2][e0 + 3]);
-          sched_fence();
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            vmx = fmaxf(fmaxf(vmx, scur[t][4 * m]), scur[t][4 * m + 1]);
+            vmx = fmaxf(fmaxf(vmx, scur[t][4 * m + 2]), scur[t][4 * m + 3]);
+          }
         }
+        sched_fence();
       }
+#pragma unroll
+      for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
+      ptail = pf[1][1];
       if constexpr (LITE) {
         // Keep the block for the next step if some valid row's block max came
         // within `threshold` of its running max (reference :983-995); the
@@ -591,6 +610,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       step(i, sA, sB);
       if (i + 1 < nblk) step(i + 1, sB, sA);
     }
+    // The last block's deferred PV MFMAs.
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
   }
   sched_fence();
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
