@@ -12,7 +12,10 @@
 //    B operand straight from registers (no shuffle).
 //  * K and the pre-transposed V_t are staged through LDS with 16-byte
 //    global->LDS DMA (global_load_lds_dwordx4) in 4-slot rings, two blocks of
-//    lead. K is stored
+//    lead. Every DMA is inline asm, waited for by explicit vmcnt waits: with
+//    one the compiler can see in flight, its wait counting turns every LDS
+//    fragment wait into lgkmcnt(0) instead of the partial count the
+//    in-order reads allow. K is stored
 //    in MFMA fragment order so every operand read is a conflict-free
 //    ds_read_b128 at base + 16*lane.
 //  * Online softmax in base 2 with the running max kept on the integer grid:
@@ -235,14 +238,14 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     if ((kb + 1) * kKvBlock <= p.Skv) {
       const char* base = kh + kb * kblk_bytes;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) dma16(base + koff[i], (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
+      for (int i = 0; i < 2; ++i) dma16_sbase(base, koff[i], st + (wave * 2 + i) * kFragBytes);
     } else {
       // Last partial block: clamp rows past Skv (they are masked in softmax).
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         int kv = kb * kKvBlock + kdma_row(i);
         kv = kv < p.Skv ? kv : p.Skv - 1;
-        dma16(kh + (long long)kv * row_stride * 2 + kdma_chunk(i) * 16, (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
+        dma16_opaque(kh + (long long)kv * row_stride * 2 + kdma_chunk(i) * 16, st + (wave * 2 + i) * kFragBytes);
       }
     }
   };
@@ -251,7 +254,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     char* st = vring + slot * kVBytes;
     const char* base = vth + (long long)kb * kVBytes;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(base + voff + i * kFragBytes, (MM_LDS void*)(st + (wave * 2 + i) * kFragBytes));
+    for (int i = 0; i < 2; ++i) dma16_sbase(base, voff + i * kFragBytes, st + (wave * 2 + i) * kFragBytes);
   };
 
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
