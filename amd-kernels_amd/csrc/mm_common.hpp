@@ -138,18 +138,15 @@ __device__ __forceinline__ float xor32_sum(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Global -> LDS DMA, 16 bytes per lane. Lane l's 16 bytes land at
-// lds_dst + 16*l; lds_dst must be wave-uniform.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void dma16(const void* gsrc, MM_LDS void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(gsrc, lds_dst, 16, 0, 0);
-}
-
-// The same DMA issued through asm, for kernels that count their loads
+// Global -> LDS DMA, 16 bytes per lane: lane l's 16 bytes land at
+// lds_dst + 16*l; lds_dst is a generic pointer into __shared__ memory,
+// wave-uniform. Issued through asm, for kernels that count their loads
 // themselves (explicit s_waitcnt vmcnt): hidden from the compiler's wait-count
-// model, it cannot trigger a conservative vmcnt(0) before LDS reads that the
-// compiler cannot prove disjoint from an in-flight DMA. lds_dst is a generic
-// pointer into __shared__ memory, wave-uniform.
+// model, an in-flight DMA can neither force a conservative vmcnt(0) before
+// LDS reads the compiler cannot prove disjoint from it nor turn the partial
+// lgkmcnt waits of in-order LDS reads into lgkmcnt(0) (both measured with
+// __builtin_amdgcn_global_load_lds).
+// ---------------------------------------------------------------------------
 __device__ __forceinline__ void dma16_opaque(const void* gsrc, const char* lds_dst) {
   const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(m0v) : "memory");
