@@ -15,9 +15,9 @@
 //    lead. Every DMA is inline asm, waited for by explicit vmcnt waits: with
 //    one the compiler can see in flight, its wait counting turns every LDS
 //    fragment wait into lgkmcnt(0) instead of the partial count the
-//    in-order reads allow. K is stored
-//    in MFMA fragment order so every operand read is a conflict-free
-//    ds_read_b128 at base + 16*lane.
+//    in-order reads allow. K slots are chunk-major in 16-row groups and V_t
+//    slots hold whole MFMA fragments in lane order, so every operand read is
+//    a conflict-free ds_read_b128.
 //  * Online softmax in base 2 with the running max kept on the integer grid:
 //    m = ceil(max(s) * log2(e)/sqrt(128)). Every rescale is an exact power of
 //    two, so the bf16 rounding of P (done with the output round mode, as in
@@ -178,7 +178,8 @@ __device__ __forceinline__ void lite_emit(const Params& p, long long row, int n,
 // so every K / V_t block is gathered once per CU. Wave w owns rows
 // [32w, 32w+32). Per 64-row kv block j:
 //     QK(j+1) MFMAs || softmax(j) VALU      then      PV(j) MFMAs
-// K and V_t stream through 4-slot LDS rings (128 KB): block j+3 is gathered
+// with the last 4 PV(j) MFMAs run after the next block barrier, ahead of
+// QK(j+2), whose first K fragment reads they cover. K and V_t stream through 4-slot LDS rings (128 KB): block j+3 is gathered
 // while block j is processed, so each DMA has two blocks of lead (measured at
 // the headline shape: 1.485 ms vs 1.621 ms for two 128-row CTAs per CU with
 // 2-slot rings and one block of lead).
