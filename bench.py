@@ -10,10 +10,13 @@ forward kernel, as the reference times it, benchmark/runner.py:176-181).
 timed with HIP events on the stream it is launched on). ``cpu_baseline`` times
 the reference repo's CPU oracle formula (examples/basic.py:16-17) over the
 whole headline workload on this host's cores (median of 3). Extra keys:
-``attention`` (every round mode, the reference benchmark's "realistic" inputs,
-the configs[3] long shapes, a shape whose tail KV-split fires, with and
-without the split, the configs[2] cross-attention shapes) and ``mla`` (configs[4] decode lines with their own CPU
-baseline, the reference test's fp32 formula).
+``attention`` (the configs[0] tiny case, every round mode, the reference
+benchmark's "realistic" inputs, the configs[3] long shapes, a shape whose tail
+KV-split fires, with and without the split, the configs[2] cross-attention
+shapes; each leg other than the headline's modes carries a ``cpu`` figure of
+the same formula on its own input bits, the whole leg or a stated subset of
+heads and rows), ``lite`` and ``mla`` (configs[4] decode lines with their own
+CPU baseline, the reference test's fp32 formula).
 """
 import argparse
 import json
@@ -146,6 +149,17 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
     from helpers import realistic_bf16
 
     res = {}
+    cpu = not args.no_cpu_baseline
+    # the tiny BHSD case (1, 2, 256, 128), RTNE.
+    g0 = torch.Generator().manual_seed(42)
+    tq, tk, tv = (torch.randn(1, 2, 256, 128, generator=g0).to(torch.bfloat16) for _ in range(3))
+    gq, gk, gv = (t.to("cuda:0") for t in (tq, tk, tv))
+    ms = _time(torch, lambda i: ma.forward(gq, gk, gv, round_mode="rtne", layout="bhsd"), args.steps, args.warmup)
+    res["tiny_1x2x256_bhsd_rtne"] = _leg("tiny 1x2x256 bhsd", 1, 2, 256, 256, ms, round_mode="rtne", layout="bhsd")
+    if cpu:
+        res["tiny_1x2x256_bhsd_rtne"]["cpu"] = cpu_attention(
+            torch, tq.transpose(1, 2), tk.transpose(1, 2), tv.transpose(1, 2))
+    del gq, gk, gv
     q, k, v = (t.to("cuda:0") for t in qkv_cpu)
     out = torch.empty_like(q)
     for mode in ("rtne", "rtna", "rtz"):
@@ -168,6 +182,12 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
         key = f"{B}x{H}x{S}"
         res[f"long_{key}_rtne"] = _leg(f"long {key} rtne", B, H, S, S, ms, round_mode="rtne",
                                        ref_mi300x_ms=REF_MI300X_MS[(key, "rtne")])
+        if cpu:
+            # One head; for the 86016-token shape its first 8192 q rows.
+            rows = S if S <= 16384 else 8192
+            res[f"long_{key}_rtne"]["cpu"] = cpu_attention(
+                torch, q[:1, :rows, :1].cpu(), k[:1, :, :1].cpu(), v[:1, :, :1].cpu())
+            res[f"long_{key}_rtne"]["cpu"]["sample"] = f"1 of {B * H} heads x {rows} of {S} q rows"
         del q, k, v, o
     # A shape whose last round of CTAs the tail planner splits: 17 q-blocks x 48
     # heads = 816 CTAs = 3 rounds of 256 + a 48-CTA tail.
@@ -185,6 +205,9 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
         finally:
             os.environ.pop("MOONMATH_NO_TAIL", None)
         res[f"tail_{label}_2x24_sq4097_skv8192_rtne"] = _leg(f"tail {label}", B, H, Sq, Skv, ms, round_mode="rtne")
+    if cpu:
+        res["tail_split_2x24_sq4097_skv8192_rtne"]["cpu"] = cpu_attention(
+            torch, q.cpu(), k.cpu(), v.cpu(), heads=[(0, h) for h in range(8)])
     del q, k, v, o
     # cross-attention, Q ~ N(0,1), K/V ~ 0.5 N(0,1). Short KV ranges
     # make these shapes partly HBM-bound (Q in, O out), so the leg also reports
@@ -200,6 +223,8 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
         res[f"cross_2x24_sq{Sq}_skv{Skv}_rtne"] = _leg(
             f"cross sq{Sq} skv{Skv}", 2, 24, Sq, Skv, ms, round_mode="rtne", hbm_bytes=nbytes,
             hbm_GBs=round(nbytes / (ms * 1e-3) / 1e9, 1))
+        if cpu:
+            res[f"cross_2x24_sq{Sq}_skv{Skv}_rtne"]["cpu"] = cpu_attention(torch, q.cpu(), k.cpu(), v.cpu())
         del q, k, v, o
     return res
 
@@ -367,6 +392,33 @@ def mla_cpu_baseline(torch, q_cpu, set_cpu, lens, nbytes, flops):
     return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "tflops": round(flops / t / 1e12, 4),
             "ms": round(t * 1e3, 1), "cores": threads, "kind": "port",
             "sample": "all 64 requests, one (Q, pool) set, median of 3 runs"}
+
+
+def cpu_attention(torch, q, k, v, heads=None, rows=None):
+    """The same CPU formula as cpu_baseline on a leg's own input bits (BSHD CPU
+    tensors): every (b, h) head and q row by default, or a stated subset
+    (`heads` (b, h) pairs, the first `rows` q rows), whose rate stands for the
+    whole leg (heads and rows are independent); median of 3 runs."""
+    threads, aff = _cpu_threads()
+    torch.set_num_threads(threads)
+    from oracle.attention import torch_formula_cpu
+
+    B, Sq, H, _ = q.shape
+    Skv = k.shape[1]
+    hs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
+    r = rows if rows is not None else Sq
+
+    def run():
+        for b, h in hs:
+            torch_formula_cpu(q[b:b + 1, :r, h].unsqueeze(1), k[b:b + 1, :, h].unsqueeze(1),
+                              v[b:b + 1, :, h].unsqueeze(1))
+
+    t = _median3(run)
+    flops = 4.0 * len(hs) * r * Skv * 128
+    whole = len(hs) == B * H and r == Sq
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "ms": round(t * 1e3, 2), "cores": threads,
+            "kind": "port",
+            "sample": "whole leg" if whole else f"{len(hs)} of {B * H} heads x {r} of {Sq} q rows ({flops:.3g} flop)"}
 
 
 def cpu_baseline(torch, qkv_cpu):
