@@ -306,6 +306,31 @@ def test_ragged_small(layout, Sq, Skv):
            f"ragged_{layout}_2x3_sq{Sq}_skv{Skv}_rtna")
 
 
+def _random_cases(n, seed):
+    """Seeded random shapes across the kernel's edges: short and ragged Sq / Skv
+    (partial 64-row KV blocks and 256-row q blocks), both layouts, every round
+    mode, K/V scaled down or up. At least 8 query rows per head, so each case
+    compares >= 1024 outputs against the fraction bars."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+        Sq = int(rng.integers(8, 64)) if rng.random() < 0.3 else int(rng.integers(64, 1500))
+        Skv = int(rng.integers(1, 64)) if rng.random() < 0.3 else int(rng.integers(64, 2500))
+        cases.append((B, H, Sq, Skv, str(rng.choice(["bhsd", "bshd"])), str(rng.choice(["rtne", "rtna", "rtz"])),
+                      float(rng.choice([0.5, 1.0, 2.0]))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(12, 2026), ids=lambda c: "b{}h{}_sq{}_skv{}_{}_{}_x{}".format(*c))
+def test_random_shapes_match_oracle(case):
+    B, H, Sq, Skv, layout, mode, kv_scale = case
+    q, k, v = _make(B, H, Sq, Skv, layout, seed=Sq * 31 + Skv, kv_scale=kv_scale)
+    out = _forward(q, k, v, mode, layout)
+    _check(q, k, v, out, mode, layout, [(b, h) for b in range(B) for h in range(H)],
+           "random_{}x{}_sq{}_skv{}_{}_{}_x{}".format(*case))
+
+
 def test_cpu_tensors_round_trip_and_out_param():
     q, k, v = _make(1, 2, 300, 200, "bhsd", seed=5)
     out_cpu = ma.forward(q, k, v, round_mode="rtne")

@@ -137,6 +137,46 @@ def test_paged_ragged_matches_oracle(q_len):
     _check(o, q_lat, q_pe, fp8_bits(pool), lens, SCALE_576, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
 
 
+def _random_mla_cases(n, seed):
+    """Seeded random decode configs across the three kernels (query rows per
+    request H * q_len: <= 16, 17..95 or > 128, 96..128), ragged lengths from 1
+    token, split budgets 1..5, both softmax scales."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        q_len = int(rng.choice([1, 1, 2, 3, 4, 8]))
+        kind = rng.integers(0, 3)
+        rows = int(rng.integers(1, 17)) if kind == 0 else (int(rng.integers(96, 129)) if kind == 1
+                                                         else int(rng.integers(17, 257)))
+        H = max(1, min(128, rows // q_len))
+        B = int(rng.integers(1, 7))
+        lens = tuple(int(x) for x in rng.integers(1, 2000, size=B))
+        cases.append((H, q_len, int(rng.integers(1, 6)), bool(rng.integers(0, 2)), lens))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_mla_cases(12, 2026),
+                         ids=lambda c: "h{}_q{}_p{}_s{}_b{}".format(c[0], c[1], c[2], 576 if c[3] else 192, len(c[4])))
+def test_random_paged_configs_match_oracle(case):
+    H, q_len, parts, s576, lens = case
+    lens = list(lens)
+    B = len(lens)
+    scale = SCALE_576 if s576 else SCALE_192
+    seed = 7 * H + q_len + sum(lens) % 997
+    pool, idx, indptr = paged_pool(lens, seed)
+    q_lat, q_pe = rand_q(B, q_len, H, seed)
+    o = torch.zeros(B, q_len, H, 512, dtype=torch.bfloat16, device=DEV)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    if q_len == 1:
+        ma.mla_decode_a16w8_paged_dev(_d(q_lat[:, 0].contiguous()), _d(q_pe[:, 0].contiguous()), _d(pool),
+                                      o[:, 0], _d(lens_t), None, _d(idx), _d(indptr), parts, scale, KV_SCALE)
+    else:
+        ma.mla_decode_a16w8_multiq_paged_dev(_d(q_lat), _d(q_pe), _d(pool), o, _d(lens_t), None, _d(idx),
+                                             _d(indptr), parts, scale, KV_SCALE)
+    torch.cuda.synchronize()
+    _check(o, q_lat, q_pe, fp8_bits(pool), lens, scale, kv_indices=idx.numpy(), kv_indptr=indptr.numpy())
+
+
 @pytest.mark.parametrize("parts", [1, 3, 7])
 def test_split_parts_agree(parts):
     """Any parts >= 1 gives results within the tolerance rule of parts = 1."""
