@@ -136,18 +136,15 @@ def _random_rows(nrows, nkb, phase, seed):
     return rows
 
 
-@pytest.mark.parametrize("phase", [1, 0])
-@pytest.mark.parametrize("mode", ["rtna", "rtz"])
-def test_lite_step_matches_oracle(phase, mode):
-    """One step over random valid read rows (ragged Sq / Skv, BSHD): output of
-    sampled tiles under the tolerance rule, and every written row exactly."""
-    Bq, Hq, Sq, Skv = 2, 3, 700, 1500
+def _lite_step_check(Bq, Hq, Sq, Skv, phase, mode, threshold, seed, row_seed, name):
+    """One step over random valid read rows (BSHD): every tile's output under
+    the tolerance rule, and every written row exactly. Returns the read rows."""
     nqb, nkb = -(-Sq // 256), -(-Skv // 64)
-    q, k, v = (randn_bf16((Bq, s, Hq, 128), 90 + i) for i, s in enumerate((Sq, Skv, Skv)))
-    rows = _random_rows(Bq * Hq * nqb, nkb, phase, seed=phase * 10 + len(mode))
+    q, k, v = (randn_bf16((Bq, s, Hq, 128), seed + i) for i, s in enumerate((Sq, Skv, Skv)))
+    rows = _random_rows(Bq * Hq * nqb, nkb, phase, seed=row_seed)
     read = torch.from_numpy(rows).view(Bq, Hq, nqb, nkb + 2).to(DEV)
     write = torch.full_like(read, -7)
-    out = ma.forward_lite(q.to(DEV), k.to(DEV), v.to(DEV), read, write, threshold=-6.0, phase=phase,
+    out = ma.forward_lite(q.to(DEV), k.to(DEV), v.to(DEV), read, write, threshold=threshold, phase=phase,
                           round_mode=mode, layout="bshd")
     torch.cuda.synchronize()
     got_rows = write.cpu().numpy().reshape(-1, nkb + 2)
@@ -158,15 +155,40 @@ def test_lite_step_matches_oracle(phase, mode):
         bh, t = divmod(w, nqb)
         b, h = divmod(bh, Hq)
         r0, r1 = t * 256, min(Sq, (t + 1) * 256)
-        o, nxt, blocks = ol.step_tile(qf[b, h, r0:r1], kf[b, h], vf[b, h], rows[w], phase, -6.0,
+        o, nxt, blocks = ol.step_tile(qf[b, h, r0:r1], kf[b, h], vf[b, h], rows[w], phase, threshold,
                                       {"rtne": 0, "rtna": 1, "rtz": 2}[mode], aux=True)
         assert list(got_rows[w, :1 + nxt[0]]) == nxt, (w, blocks)
         ref, _, scl, tie = o
         stats.append(compare_bf16(got[b, h, r0:r1], ref, scl, tie, fractions=False))
     agg = aggregate_stats(stats)
-    log_stats(f"lite_step_2x3_sq700_skv1500_phase{phase}_{mode}", agg)
+    log_stats(name, agg)
     check_fractions(agg)
+    return rows, nkb
+
+
+@pytest.mark.parametrize("phase", [1, 0])
+@pytest.mark.parametrize("mode", ["rtna", "rtz"])
+def test_lite_step_matches_oracle(phase, mode):
+    """One step over random valid read rows (ragged Sq / Skv, BSHD): output of
+    every tile under the tolerance rule, and every written row exactly."""
+    rows, nkb = _lite_step_check(2, 3, 700, 1500, phase, mode, -6.0, 90, phase * 10 + len(mode),
+                                 f"lite_step_2x3_sq700_skv1500_phase{phase}_{mode}")
     assert any(len(ol.decode(r, nkb, phase)[0]) < nkb for r in rows)
+
+
+def _random_lite_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 3)), int(rng.integers(1, 3)), int(rng.integers(8, 900)), int(rng.integers(1, 2500)),
+             int(rng.integers(0, 2)), str(rng.choice(["rtne", "rtna", "rtz"])), float(rng.choice([-8.0, -3.0, 0.0])))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("case", _random_lite_cases(6, 2026), ids=lambda c: "b{}h{}_sq{}_skv{}_ph{}_{}_t{}".format(*c))
+def test_lite_random_shapes_match_oracle(case):
+    """Seeded random shapes, phases, round modes and thresholds for one step."""
+    Bq, Hq, Sq, Skv, phase, mode, thr = case
+    _lite_step_check(Bq, Hq, Sq, Skv, phase, mode, thr, Sq + Skv, Sq * 3 + Skv,
+                     "lite_random_{}x{}_sq{}_skv{}_ph{}_{}_t{}".format(*case))
 
 
 def _lpt_rows(kind, nrows, nkb):
