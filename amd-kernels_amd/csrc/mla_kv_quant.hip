@@ -52,12 +52,13 @@ __global__ __launch_bounds__(kThreads) void kv_quant_kernel(const uint16_t* __re
   if (item >= n_tokens * kChunks) return;
   const long long tok = item / kChunks;
   const int chunk = (int)(item - tok * kChunks);
-  const long long slot = slots[tok];
-  if (slot < 0 || slot >= num_slots) return;  // padding token / outside the pool: nothing written
   const uint16_t* src = chunk < kLat / 16 ? c_kv + tok * kLat + chunk * 16 : k_pe + tok * kRope + (chunk - kLat / 16) * 16;
-  // Inputs are read once and rows written once: non-temporal accesses.
+  // Inputs are read once and rows written once: non-temporal accesses. The
+  // row loads go out together with the slot load (neither depends on the
+  // other), so a thread waits one memory round trip, not two.
   const u32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));      // elements 0..7
   const u32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 8));  // elements 8..15
+  const long long slot = slots[tok];
   auto val = [&](uint32_t pair, bool upper) {  // one bf16 of a pair, widened and divided by kv_scale
     const float xv = __builtin_bit_cast(float, upper ? (pair & 0xFFFF0000u) : (pair << 16));
     const float x = POW2 ? xv * inv_scale : xv / kv_scale;
@@ -72,6 +73,10 @@ __global__ __launch_bounds__(kThreads) void kv_quant_kernel(const uint16_t* __re
     r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, val(p1, false), val(p1, true), 1.0f, true);
     out[w] = __builtin_bit_cast(uint32_t, r);
   }
+  // The converted row exists before the slot test (an empty asm use), so the
+  // compiler cannot sink the row loads behind the slot's round trip.
+  asm volatile("" ::"v"(out));
+  if (slot < 0 || slot >= num_slots) return;  // padding token / outside the pool: nothing written
   __builtin_nontemporal_store(out, reinterpret_cast<u32x4*>(pool + slot * kRow + chunk * 16));
 }
 
