@@ -371,7 +371,8 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   float row_m = kNegFltMax, row_l = 0.f;
 
   // Lite vote state: each row's exact running max of s*c (log2 units) over the
-  // blocks processed so far (reference softmax_update's row_max, :398-436).
+  // blocks this wave kept so far (reference softmax_update's row_max,
+  // :398-436, which a dropped block never reaches).
   float run_mx = -__builtin_inff();
   const bool row_valid = q_row0 + r < p.Sq;
 
@@ -382,6 +383,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // Zero before the first block, so those MFMAs then add exact zeros.
   bf16x8 vtail[4] = {};
   bf16x8 ptail = {};
+  // Lite: whether the previous block's deferred MFMAs carry a kept block
+  // (wave-uniform; a dropped block leaves nothing to add).
+  bool tail_on = false;
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
@@ -519,12 +523,17 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // The previous block's last 4 PV MFMAs (operands in registers since
       // before the barrier) cover the latency of these first K reads:
       // 1.435 -> 1.411 ms at the headline shape (RTNA, one box).
+      if (!LITE || tail_on) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
-        sched_fence();
+        for (int dt = 0; dt < 4; ++dt) {
+          oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
+          sched_fence();
+        }
       }
       bf16x8 vb[4];
+      // Lite: the block max of the vote, folded over the QK steps (4 scores
+      // per step).
+      float vmx = -__builtin_inff();
 #pragma unroll
       for (int ds = 0; ds < 8; ++ds) {
         bf16x8 nk0, nk1;
@@ -538,6 +547,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         }
         snext[0] = mfma32(kf0, qf[ds], snext[0]);
         sm_pair(0, ds, neg_m0);
+        if constexpr (LITE) {
+          const int t = ds >> 2, e0 = 4 * (ds & 3);
+          vmx = fmaxf(fmaxf(vmx, scur[t][e0]), scur[t][e0 + 1]);
+          vmx = fmaxf(fmaxf(vmx, scur[t][e0 + 2]), scur[t][e0 + 3]);
+        }
         if (ds & 1) dma3_step(ds >> 1);
         snext[1] = mfma32(kf1, qf[ds], snext[1]);
         if (ds & 1) sm_pair(1, ds >> 1, neg_m0);
@@ -549,74 +563,80 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       pack_pf(0);
       __builtin_amdgcn_s_setprio(0);
-      // Wave-uniform growth tests: row tile 0 and the first half of row tile 1
-      // before any PV of this block, the second half of row tile 1 before its PV.
-      if (__builtin_amdgcn_ballot_w64(fmaxf(lpart[0] + lpart[1], lpart[2]) > kGrowLimit) != 0) {
-        rebase(0, 3);
-        pack_pf(0);
-      }
-      const float neg_m1 = -row_m;
-      // PV of row tile 0 (k-step ss, d-tile dt) with softmax pairs 4..7 of tile 1.
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const int ss = m >> 2, dt = m & 3;
-        const bf16x8 a = vb[m & 3];
-        vb[m & 3] = vfrag_n(m + 4);
-        oacc[dt] = mfma32(a, pf[0][ss], oacc[dt]);
-        if (m < 4) sm_pair(1, 4 + m, neg_m1);
-        sched_fence();
-      }
-      if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
-      pack_pf(1);
-      // PV of row tile 1, k-step 0 (k-step 1 runs after the next barrier, from
-      // vtail / ptail); lite: with the block max of the vote (8 scores per MFMA).
-      float vmx = -__builtin_inff();
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const bf16x8 a = vb[m];
-        vb[m] = vfrag_n(12 + m);
-        oacc[m] = mfma32(a, pf[1][0], oacc[m]);
-        if constexpr (LITE) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            vmx = fmaxf(fmaxf(vmx, scur[t][4 * m]), scur[t][4 * m + 1]);
-            vmx = fmaxf(fmaxf(vmx, scur[t][4 * m + 2]), scur[t][4 * m + 3]);
-          }
-        }
-        sched_fence();
-      }
-#pragma unroll
-      for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
-      ptail = pf[1][1];
+      // Lite vote, decided before any PV, rebase or sum of this block (per-wave
+      // soft skip, reference :983-1001 and :891-898): the wave keeps the block
+      // if some valid row's block max came within `threshold` of the row's
+      // running max over the blocks this wave kept before it; the first
+      // processed block is always kept. bm and bm - run_mx are each rounded to
+      // fp32 (no fused multiply-subtract). A block the wave drops adds nothing
+      // to its rows: no PV MFMAs (its deferred tail included), no l, no max
+      // change. The wave's bit in the block's LDS vote byte feeds the next
+      // step's list.
+      bool wkeep = true;
       if constexpr (LITE) {
-        // Keep the block for the next step if some valid row's block max came
-        // within `threshold` of its running max (reference :983-995); the
-        // first processed block is always kept. bm and bm - run_mx are each
-        // rounded to fp32 (no fused multiply-subtract).
 #pragma clang fp contract(off)
         const float bm = xor32_max(vmx) * c;
         const bool keep = row_valid && (bm - run_mx > p.threshold);
-        run_mx = fmaxf(run_mx, bm);
-        if ((__builtin_amdgcn_ballot_w64(keep) != 0 || i == 0) && lane == 0) {
-          // Set the wave's bit in the block's vote byte. Inline asm: the
-          // compiler would put a vmcnt(0) wait (for the in-flight K/V DMAs,
-          // which also write LDS) before an atomic it can see. The DMAs never
-          // touch the vote bytes; lite_emit reads them after lgkmcnt(0) and a
-          // barrier.
-          const uint32_t va = (uint32_t)(uintptr_t)(MM_LDS uint8_t*)(lite_vote + ((i >> 2) << 2));
-          const uint32_t vbits = (1u << wave) << ((i & 3) * 8);
-          asm volatile("ds_or_b32 %0, %1" ::"v"(va), "v"(vbits) : "memory");
+        wkeep = __builtin_amdgcn_ballot_w64(keep) != 0 || i == 0;
+        if (wkeep) {
+          run_mx = fmaxf(run_mx, bm);
+          if (lane == 0) {
+            // Inline asm: the compiler would put a vmcnt(0) wait (for the
+            // in-flight K/V DMAs, which also write LDS) before an atomic it
+            // can see. The DMAs never touch the vote bytes; lite_emit reads
+            // them after lgkmcnt(0) and a barrier.
+            const uint32_t va = (uint32_t)(uintptr_t)(MM_LDS uint8_t*)(lite_vote + ((i >> 2) << 2));
+            const uint32_t vbits = (1u << wave) << ((i & 3) * 8);
+            asm volatile("ds_or_b32 %0, %1" ::"v"(va), "v"(vbits) : "memory");
+          }
         }
+        tail_on = wkeep;
       }
-      row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+      if (wkeep) {
+        // Wave-uniform growth tests: row tile 0 and the first half of row tile
+        // 1 before any PV of this block, the second half of row tile 1 before
+        // its PV.
+        if (__builtin_amdgcn_ballot_w64(fmaxf(lpart[0] + lpart[1], lpart[2]) > kGrowLimit) != 0) {
+          rebase(0, 3);
+          pack_pf(0);
+        }
+        const float neg_m1 = -row_m;
+        // PV of row tile 0 (k-step ss, d-tile dt) with softmax pairs 4..7 of tile 1.
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const int ss = m >> 2, dt = m & 3;
+          const bf16x8 a = vb[m & 3];
+          vb[m & 3] = vfrag_n(m + 4);
+          oacc[dt] = mfma32(a, pf[0][ss], oacc[dt]);
+          if (m < 4) sm_pair(1, 4 + m, neg_m1);
+          sched_fence();
+        }
+        if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
+        pack_pf(1);
+        // PV of row tile 1, k-step 0 (k-step 1 runs after the next barrier,
+        // from vtail / ptail).
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const bf16x8 a = vb[m];
+          vb[m] = vfrag_n(12 + m);
+          oacc[m] = mfma32(a, pf[1][0], oacc[m]);
+          sched_fence();
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
+        ptail = pf[1][1];
+        row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+      }
     };
     for (int i = 0; i < nblk; i += 2) {
       step(i, sA, sB);
       if (i + 1 < nblk) step(i + 1, sB, sA);
     }
     // The last block's deferred PV MFMAs.
+    if (!LITE || tail_on) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
+      for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
+    }
   }
   sched_fence();
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -753,7 +773,13 @@ __global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const int16_t* 
     for (int u = 0; u < 4; ++u) {
       const int w = wb + u * kLptThreads;
       if (w < nctas) {
-        const int bk = lite_kept(read_list + (long long)w * (nkb + 2), nkb, e[u]) * kLptBuckets / (nkb + 1);
+        // A row's kept count is at most the sum of |end - start| over its
+        // (nkb + 1) / 2 pairs of int16 ids (< 2^28); counts past nkb land in
+        // the top bucket anyway, so clamping first keeps the product in range
+        // for any row content.
+        int kept = lite_kept(read_list + (long long)w * (nkb + 2), nkb, e[u]);
+        kept = kept < nkb + 1 ? kept : nkb + 1;
+        const int bk = kept * kLptBuckets / (nkb + 1);
         bk_of[w] = (uint8_t)(bk < kLptBuckets ? bk : kLptBuckets - 1);
       }
     }

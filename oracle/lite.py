@@ -8,9 +8,18 @@ Restates, for one (b, h, q-tile), the reference's skip-list semantics:
   row; range (s, e) yields s+d, s+2d, ... while strictly before e+d and at
   least once, d = +1 in phase 1 and -1 in phase 0. Ids outside [0, nkb) are
   dropped (this build's guard; a writer never produces them).
-* ``votes``: keep flags (reference softmax :983-995): block i is kept when some
-  valid row's fp32 block max times c, minus the row's running max of the same
-  over the blocks before it, exceeds ``threshold``; the first block always.
+* ``wave_keep`` / ``votes``: the per-wave soft skip and the tile's vote
+  (reference softmax :983-1001 and pv_phase :891-898). The tile's q rows are
+  taken in wave groups of ``WAVE_ROWS`` (this build's wave owns 32 rows; the
+  reference's owns 48). A wave keeps processed block i when i == 0 or when
+  some valid row of the wave has fl32(fl32(bm * c) - run) > ``threshold``,
+  with bm the row's fp32 max over the block's valid keys and run the row's
+  running max of fl32(bm * c) over the blocks THIS WAVE kept before i. A
+  block the wave does not keep adds nothing to the wave's rows (no PV, no
+  denominator, no max change). The tile's vote for the next list is the OR of
+  its waves' keep flags.
+* ``forward_tile`` / ``step_tile``: each wave's rows are attention over the
+  keys of the blocks that wave kept.
 * ``emit``: the next row (reference record(), :685-716): a marker at every
   change of the skip state, which restarts as "skip" after each range end; a
   kept range-end block also writes block + d; ``must_do`` ranges [s, e) force
@@ -18,8 +27,6 @@ Restates, for one (b, h, q-tile), the reference's skip-list semantics:
 * ``kept_count`` / ``lpt_order``: the work count of a row (sum of |hi - lo| over
   its pairs, reference plan_lite_order :1314-1326) and the heaviest-first CTA
   order over 64 buckets of kept / (nkb + 1), stable in CTA index.
-* ``forward_tile``: the tile's output = the attention oracle over the keys of
-  the processed blocks.
 
 ``seed_row`` is the compute-all row LiteAttention starts from
 (reference moonmath_attention/lite.py:141-147).
@@ -32,6 +39,7 @@ KV_BLOCK = 64
 Q_TILE = 256
 MAX_BLOCKS = 8192
 LPT_BUCKETS = 64
+WAVE_ROWS = 32
 
 
 def seed_row(nkb):
@@ -68,17 +76,38 @@ def block_max_log2(s32, blocks, skv):
     return np.array(out, dtype=np.float32).reshape(len(blocks), s32.shape[0])
 
 
-def votes(s32_valid, blocks, skv, threshold):
-    """s32_valid: fp32 scores [valid rows of the tile, Skv]."""
-    bms = block_max_log2(s32_valid, blocks, skv)
-    run = np.full(s32_valid.shape[0], -np.inf, dtype=np.float32)
+def wave_keep(s32_wave, blocks, skv, threshold):
+    """Keep flags of one wave over the processed blocks. s32_wave: fp32 scores
+    [valid rows of the wave, Skv] (no rows: only the first block is kept)."""
+    bms = block_max_log2(s32_wave, blocks, skv)
+    run = np.full(s32_wave.shape[0], -np.inf, dtype=np.float32)
     thr = np.float32(threshold)
     keep = []
     with np.errstate(invalid="ignore", over="ignore"):
         for i, bm in enumerate(bms):
-            k = bool(((bm - run) > thr).any())
-            run = np.fmax(run, bm)
-            keep.append(i == 0 or k)
+            k = i == 0 or bool(((bm - run) > thr).any())
+            if k:
+                run = np.fmax(run, bm)
+            keep.append(k)
+    return keep
+
+
+def wave_groups(nrows):
+    """Row ranges [r0, r1) of the tile's waves that hold valid rows."""
+    return [(r0, min(nrows, r0 + WAVE_ROWS)) for r0 in range(0, nrows, WAVE_ROWS)]
+
+
+def wave_keeps(s32_valid, blocks, skv, threshold):
+    """[(r0, r1, keep flags)] for every wave with valid rows."""
+    return [(r0, r1, wave_keep(s32_valid[r0:r1], blocks, skv, threshold)) for r0, r1 in wave_groups(s32_valid.shape[0])]
+
+
+def votes(s32_valid, blocks, skv, threshold):
+    """The tile's vote: block i stays in the next list when some wave kept it.
+    s32_valid: fp32 scores [valid rows of the tile, Skv]."""
+    keep = [False] * len(blocks)
+    for _, _, kw in wave_keeps(s32_valid, blocks, skv, threshold):
+        keep = [a or b for a, b in zip(keep, kw)]
     return keep
 
 
@@ -126,7 +155,7 @@ def scores(q_rows, k_head):
 
 
 def forward_tile(q_rows, k_head, v_head, blocks, mode, aux=False):
-    """The tile's output over the keys of ``blocks`` (order irrelevant)."""
+    """Rows' output over the keys of ``blocks`` (order irrelevant)."""
     skv = k_head.shape[0]
     idx = np.concatenate([np.arange(b * KV_BLOCK, min(skv, (b + 1) * KV_BLOCK)) for b in blocks]) \
         if blocks else np.zeros(0, dtype=np.int64)
@@ -137,10 +166,34 @@ def forward_tile(q_rows, k_head, v_head, blocks, mode, aux=False):
     return res if aux else res[0]
 
 
-def step_tile(q_rows_valid, k_head, v_head, row, phase, threshold, mode, must_do=None, aux=False):
-    """One lite step of one tile: (output bits, next row, processed blocks)."""
+def step_tile(q_rows_valid, k_head, v_head, row, phase, threshold, mode, must_do=None, aux=False, s32=None):
+    """One lite step of one tile: (output bits, next row, processed blocks).
+    The output (and, with ``aux``, pre / scale / tie) stacks the waves' rows,
+    each wave over the blocks it kept. ``s32``: the tile's ``scores``, if the
+    caller already has them."""
     nkb = -(-k_head.shape[0] // KV_BLOCK)
     blocks, ends = decode(row, nkb, phase)
-    keep = votes(scores(q_rows_valid, k_head), blocks, k_head.shape[0], threshold) if blocks else []
+    if not blocks:
+        return forward_tile(q_rows_valid, k_head, v_head, [], mode, aux=aux), emit([], [], [], phase, nkb, must_do), []
+    s32 = scores(q_rows_valid, k_head) if s32 is None else s32
+    waves = wave_keeps(s32, blocks, k_head.shape[0], threshold)
+    keep = [any(kw[i] for _, _, kw in waves) for i in range(len(blocks))]
     nxt = emit(blocks, ends, keep, phase, nkb, must_do)
-    return forward_tile(q_rows_valid, k_head, v_head, blocks, mode, aux=aux), nxt, blocks
+    parts = [forward_tile(q_rows_valid[r0:r1], k_head, v_head, [b for b, k in zip(blocks, kw) if k], mode, aux=True)
+             for r0, r1, kw in waves]
+    out = np.concatenate([pt[0] for pt in parts])
+    if not aux:
+        return out, nxt, blocks
+    res = (out, None) + tuple(np.concatenate([pt[j] for pt in parts]) for j in (2, 3))
+    return res, nxt, blocks
+
+
+def wave_blocks(q_rows_valid, k_head, row, phase, threshold, s32=None):
+    """The blocks each wave of the tile kept: [(r0, r1, [block ids])]."""
+    nkb = -(-k_head.shape[0] // KV_BLOCK)
+    blocks, _ = decode(row, nkb, phase)
+    if not blocks:
+        return [(r0, r1, []) for r0, r1 in wave_groups(q_rows_valid.shape[0])]
+    s32 = scores(q_rows_valid, k_head) if s32 is None else s32
+    waves = wave_keeps(s32, blocks, k_head.shape[0], threshold)
+    return [(r0, r1, [b for b, k in zip(blocks, kw) if k]) for r0, r1, kw in waves]

@@ -1,13 +1,17 @@
 """GPU tests of LiteAttention (forward_lite + LiteAttention + LPT order).
 
 The reference's contracts (tests/test_attention.py:88-214), on this build's
-256-row tiles: the compute-all seed step equals the dense forward (here
-bit-identical, the reference checks against SDPA); the LPT order is
+256-row tiles and 32-row waves: the compute-all seed step on well-spread
+inputs equals the dense forward (bit-identical here, once the oracle confirms
+no wave drops a block; the reference checks against SDPA); the LPT order is
 bit-identical to the plain order; a must_do list pinning every block
-reproduces compute-all at every step; the learned list keeps exactly the hot
-blocks of each head. Beyond them: steps over non-trivial read lists in both
-phases against the oracle (output under the tolerance rule, written rows
-exactly), and the LPT permutation against the oracle's.
+reproduces the compute-all step; the learned list keeps exactly the hot
+blocks of each head. Beyond them: five LiteAttention steps on the reference's
+peaked inputs, where the per-wave soft skip drops the cold blocks inside
+every step, against the oracle at every step in two modes; single steps over
+non-trivial read lists in both phases (output under the tolerance rule,
+written rows exactly); and the LPT permutation against the oracle's,
+including rows whose counts are far past the block count.
 """
 import numpy as np
 import pytest
@@ -74,6 +78,12 @@ def test_lite_compute_all_equals_dense_forward(layout, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(lite.view(torch.int16), dense.view(torch.int16))
     got = to_bhsd(bits(lite), layout)
+    qb_, kb_ = (to_bhsd(f32(t), layout) for t in (q, k))
+    nkb = S // 64
+    for b, h in ((0, 0), (0, 5)):
+        for t in range(S // 256):
+            waves = ol.wave_blocks(qb_[b, h, 256 * t:256 * t + 256], kb_[b, h], ol.seed_row(nkb), 1, THR)
+            assert all(kb == list(range(nkb)) for _, _, kb in waves), (b, h, t)
     stats = []
     for b, h in ((0, 0), (0, 5)):
         ref, _, scl, tie = oa.forward(f32(q), f32(k), f32(v), "rtna", layout=layout, heads=[(b, h)], aux=True)
@@ -81,6 +91,49 @@ def test_lite_compute_all_equals_dense_forward(layout, monkeypatch):
     agg = aggregate_stats(stats)
     log_stats(f"lite_compute_all_1x8x4096_{layout}_rtna", agg)
     check_fractions(agg)
+
+
+@pytest.mark.parametrize("mode", ["rtna", "rtz"])
+def test_lite_peaked_steps_match_oracle(mode):
+    """Five LiteAttention steps on the reference's peaked inputs (head h: K
+    blocks 0..h hot, the rest damped), phases 1, 0, 1, 0, 1. In the first
+    (compute-all) step every wave drops the cold blocks it reaches after the
+    hot ones, which carry most of the softmax mass, so the output is far from
+    full attention; in descending steps the cold blocks walked before the hot
+    ones are kept. At every step: every tile's output under the tolerance
+    rule against the oracle's per-wave computation, and every written row
+    exactly."""
+    q, k, v = _peaked()
+    nkb, nqb = S // 64, S // 256
+    mcode = {"rtne": 0, "rtna": 1, "rtz": 2}[mode]
+    qf, kf, vf = (to_bhsd(f32(t), "bshd") for t in (q, k, v))
+    s32 = {(h, t): ol.scores(qf[0, h, 256 * t:256 * t + 256], kf[0, h]) for h in range(H) for t in range(nqb)}
+    attn = ma.LiteAttention(threshold=THR, round_mode=mode, layout="bshd")
+    rows = np.tile(ol.seed_row(nkb), (H, nqb, 1))
+    dropped_in_step0 = 0
+    for step in range(STEPS):
+        phase = 1 - attn._phase
+        out = attn(q, k, v)
+        torch.cuda.synchronize()
+        got = to_bhsd(bits(out), "bshd")
+        written = attn.read_list.cpu().numpy()[0]
+        stats = []
+        for h in range(H):
+            for t in range(nqb):
+                r0 = 256 * t
+                o, nxt, blocks = ol.step_tile(qf[0, h, r0:r0 + 256], kf[0, h], vf[0, h], rows[h, t], phase, THR, mcode,
+                                              aux=True, s32=s32[h, t])
+                assert list(written[h, t, :1 + nxt[0]]) == nxt, (step, h, t)
+                ref, _, scl, tie = o
+                stats.append(compare_bf16(got[0, h, r0:r0 + 256], ref, scl, tie, fractions=False))
+                if step == 0:
+                    waves = ol.wave_blocks(qf[0, h, r0:r0 + 256], kf[0, h], rows[h, t], phase, THR, s32=s32[h, t])
+                    dropped_in_step0 += sum(len(kb) < nkb for _, _, kb in waves)
+        agg = aggregate_stats(stats)
+        log_stats(f"lite_peaked_1x8x4096_step{step}_phase{phase}_{mode}", agg)
+        check_fractions(agg)
+        rows = written.copy()
+    assert dropped_in_step0 == H * nqb * 8  # every wave dropped blocks inside the compute-all step
 
 
 def test_lite_lpt_matches_plain_bitexact(monkeypatch):
@@ -211,14 +264,32 @@ def _lpt_rows(kind, nrows, nkb):
     return rows
 
 
-@pytest.mark.parametrize("kind", ["counts", "mixed"])
+def _extreme_rows(nrows, nkb):
+    """Rows whose pair sums are far past nkb (alternating int16 extremes over
+    the whole row: a count near 2^28), next to ordinary and empty rows."""
+    rows = np.zeros((nrows, nkb + 2), np.int16)
+    rows[0, 0] = nkb + 1
+    rows[0, 1:] = np.where(np.arange(nkb + 1) % 2 == 0, 32767, -32768)
+    rows[1, :3] = (2, 9, -1)
+    rows[2, :3] = (2, nkb - 1, -1)
+    rows[3, 0] = -5
+    for i in range(4, nrows):
+        rows[i] = rows[i % 4]
+    return rows
+
+
+@pytest.mark.parametrize("kind", ["counts", "mixed", "extreme2048", "extreme8192"])
 def test_lite_lpt_order_matches_oracle(kind):
     """The planning kernel's CTA permutation (through the C ABI) against the
     oracle's stable heaviest-first order, on rows of very different weights
-    (one range each, or many ranges and out-of-range lengths)."""
+    (one range each, or many ranges and out-of-range lengths, or counts of
+    ~2^28 at 2048 and 8192 blocks, whose bucket product would overflow int32
+    without the clamp)."""
     Bq, Hq, Sq, Skv = 1, 6, 1024, 4096
+    if kind.startswith("extreme"):
+        Hq, Skv = 1, 64 * int(kind[len("extreme"):])
     nqb, nkb = Sq // 256, Skv // 64
-    rows = _lpt_rows(kind, Bq * Hq * nqb, nkb)
+    rows = _extreme_rows(Bq * Hq * nqb, nkb) if kind.startswith("extreme") else _lpt_rows(kind, Bq * Hq * nqb, nkb)
     assert kind == "counts" or max(int(r[0]) for r in rows) > 9
     q, k, v = (randn_bf16((Bq, s, Hq, 128), 50 + i).to(DEV) for i, s in enumerate((Sq, Skv, Skv)))
     vt = torch.empty(_lib.lib.moonmath_attention_vt_bytes(Bq, Hq, Skv) // 2, dtype=torch.bfloat16, device=DEV)

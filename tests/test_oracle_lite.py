@@ -144,3 +144,138 @@ def test_forward_tile_subset_equals_dense_oracle_on_kept_keys():
     # a planted mistake (off-by-one block) does not match
     wrong = oa.head_forward(q, k[64:192], v[64:192], 1)[0]
     assert not np.array_equal(ol.forward_tile(q, k, v, [0, 2], 1), wrong)
+
+
+def _bf(x):
+    return torch.as_tensor(x, dtype=torch.float32).to(torch.bfloat16).float().numpy()
+
+
+def _two_wave_case():
+    """64 valid rows (two waves), 2 blocks. Block 0 is hot for every row; block
+    1 is hot only for rows 0..15 (score 32 on dim 0) and scores 0 for the rest,
+    5 log2 units below their running max (fl(32 c) = 4.08, m = 5)."""
+    q = np.zeros((64, 128), np.float32)
+    q[:16, 0] = 1.0
+    q[16:, 1] = 1.0
+    k = np.zeros((128, 128), np.float32)
+    k[:64, 0] = 32.0
+    k[:64, 1] = 32.0
+    k[64:, 0] = 32.0
+    g = torch.Generator().manual_seed(11)
+    v = _bf(torch.randn(128, 128, generator=g))
+    return q, k, v
+
+
+def test_soft_skip_is_per_wave_of_32_rows():
+    """Wave 0 (rows 0..31) keeps block 1 because rows 0..15 are within the
+    threshold, so rows 16..31 see it too; wave 1 (rows 32..63) drops it and its
+    rows are attention over block 0 alone. The tile's vote keeps both blocks.
+    Expected values are the dense oracle on the stated key sets; a per-row
+    skip, 16- or 48-row waves, or no soft skip (the whole list for every row)
+    each give a different output, so each such mistake fails."""
+    q, k, v = _two_wave_case()
+    row = ol.seed_row(2)
+    out, nxt, blocks = ol.step_tile(q, k, v, row, 1, -3.0, 1)
+    assert blocks == [0, 1]
+    both = oa.head_forward(q, k, v, 1)[0]
+    first = oa.head_forward(q, k[:64], v[:64], 1)[0]
+    assert np.array_equal(out[:32], both[:32])
+    assert np.array_equal(out[32:], first[32:])
+    assert nxt == ol.emit(blocks, [False, True], [True, True], 1, 2)
+    assert [kb for _, _, kb in ol.wave_blocks(q, k, row, 1, -3.0)] == [[0, 1], [0]]
+    # The mistakes a grouping or skip error would make differ from the oracle.
+    per_row = np.concatenate([both[:16], first[16:]])
+    rows48 = np.concatenate([both[:48], first[48:]])
+    assert not np.array_equal(out, per_row)  # also what 16-row waves give
+    assert not np.array_equal(out, rows48)
+    assert not np.array_equal(out, both)  # no soft skip
+
+
+def test_soft_skip_keeps_the_running_max_of_kept_blocks_only():
+    """At threshold 0 a block can be dropped while its max is above the
+    running max (block max 4.08 after 4.09): the wave's running max must stay
+    that of the kept blocks, so block 2 (4.085) is compared with 4.09, not
+    with block 1's max. One row, scores in log2 units x / c."""
+    c = float(oa.SCALE_LOG2E)
+    s = np.array([[4.08 / c] * 64 + [4.09 / c] * 64 + [4.06 / c] * 64 + [4.085 / c] * 64], np.float32)
+    # block 1 > block 0 (kept, run = 4.09); block 2 below (dropped); block 3 below run (dropped)
+    assert ol.wave_keep(s, [0, 1, 2, 3], 256, 0.0) == [True, True, False, False]
+    # order 1, 0, 3: block 0 and 3 are below 4.09 -> dropped
+    assert ol.wave_keep(s, [1, 0, 3], 256, 0.0) == [True, False, False]
+    # with threshold -0.1 everything within 0.1 of the running max is kept
+    assert ol.wave_keep(s, [1, 0, 2, 3], 256, -0.1) == [True, True, True, True]
+
+
+def test_very_negative_threshold_is_attention_over_the_listed_blocks():
+    """No wave drops a listed block at threshold -1e30: each tile is the dense
+    oracle over exactly the keys its read row names."""
+    g = torch.Generator().manual_seed(9)
+    skv = 300
+    q, k, v = (_bf(torch.randn(n, 128, generator=g)) for n in (100, skv, skv))
+    b0, e0 = ol.decode(ol.seed_row(5), 5, 1)
+    row = np.array(ol.emit(b0, e0, [True, False, True, True, False], 1, 5) + [0] * 7, np.int16)[:7]
+    blocks, _ = ol.decode(row, 5, 0)  # read back in phase 0: 3, 2, 0
+    out, _, got_blocks = ol.step_tile(q, k, v, row, 0, -1e30, 0)
+    keys = np.concatenate([np.arange(64 * b, min(64 * b + 64, skv)) for b in sorted(blocks)])
+    assert got_blocks == blocks == [3, 2, 0]
+    assert np.array_equal(out, oa.head_forward(q, k[keys], v[keys], 0)[0])
+
+
+def _peaked_head(h, H=8, S=4096):
+    """Reference _lite_qkv_peaked (tests/test_attention.py:107-127) for one
+    head h: seed 7, K-blocks 0..h at scale 2, the rest at 0.05, bf16."""
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(1, S, H, 128, generator=g) for _ in range(3))
+    scale = torch.full((H, S), 0.05)
+    for hh in range(H):
+        scale[hh, : (hh + 1) * 64] = 2.0
+    k = k * scale.t().view(1, S, H, 1)
+    return tuple(t.to(torch.bfloat16).float().numpy()[0, :, h] for t in (q, k, v))
+
+
+def test_peaked_head0_compute_all_is_attention_over_the_hot_block():
+    """Reference peaked inputs, head 0, compute-all step: block 0 is hot (K at
+    scale 2), blocks 1..63 cold (0.05). For a wave where every row's best cold
+    score is more than 3 log2 units (plus a margin) below its block-0 maximum,
+    the soft skip must drop every cold block, so the wave's rows are exactly
+    dense attention over keys 0..63 -- while full attention differs there (the
+    4032 cold keys carry most of the softmax mass). The margin test uses plain
+    numpy maxima, independent of the vote code."""
+    q, k, v = _peaked_head(0)
+    c = float(oa.SCALE_LOG2E)
+    nkb = 64
+    hot = oa.head_forward(q[:512], k[:64], v[:64], 1)[0]
+    checked = 0
+    for t in range(2):  # tiles 0 and 1 (rows 0..511)
+        qt = q[256 * t: 256 * t + 256]
+        s = qt.astype(np.float64) @ k.astype(np.float64).T * c
+        out, nxt, blocks = ol.step_tile(qt, k, v, ol.seed_row(nkb), 1, -3.0, 1)
+        assert blocks == list(range(nkb))
+        for r0 in range(0, 256, 32):
+            gap = (s[r0:r0 + 32, 64:].max(axis=1) - s[r0:r0 + 32, :64].max(axis=1)).max()
+            if gap < -3.01:
+                checked += 1
+                assert np.array_equal(out[r0:r0 + 32], hot[256 * t + r0: 256 * t + r0 + 32]), (t, r0)
+        # the tile's next list keeps block 0 and (since some wave kept nothing else) is short
+        assert ol.kept_count(nxt, nkb) < nkb
+    assert checked >= 12
+    full = oa.head_forward(q[:64], k, v, 1)[0]
+    assert (full != hot[:64]).mean() > 0.5
+
+
+def test_lpt_bucket_arithmetic_fits_int32_for_any_row():
+    """The planning kernel sums |end - start| over at most (nkb + 1) / 2 pairs
+    of int16 ids in int32 (< 2^28 for nkb <= 8192), clamps the count to nkb + 1
+    and only then multiplies by the 64 buckets (< 2^20): no intermediate can
+    overflow, and the clamp does not change the oracle's bucket (counts past
+    nkb already land in the top bucket)."""
+    for nkb in (2048, 8192):
+        row = np.zeros(nkb + 2, np.int16)
+        row[0] = nkb + 1
+        row[1:] = np.where(np.arange(nkb + 1) % 2 == 0, 32767, -32768)
+        kept = ol.kept_count(row, nkb)
+        assert kept == (nkb // 2) * 65535 < 2 ** 28
+        assert kept * ol.LPT_BUCKETS >= 2 ** 31  # the unclamped product would wrap
+        assert (nkb + 1) * ol.LPT_BUCKETS < 2 ** 31
+        for k in (nkb, nkb + 1, kept):
+            assert min(k * ol.LPT_BUCKETS // (nkb + 1), 63) == min(min(k, nkb + 1) * ol.LPT_BUCKETS // (nkb + 1), 63)
