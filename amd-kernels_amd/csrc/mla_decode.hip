@@ -861,10 +861,10 @@ int clamp_parts(int parts, int B, int H, int q_len, bool have_ws) {
   return p;
 }
 
-int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, const void* seq_lens,
-           const void* rows, const void* kv_indices, const void* kv_indptr, int B, int H, int S_fixed, int parts,
-           int q_len, int lat_dim, int rope_dim, float scale, float kv_scale, void* workspace, void* stream,
-           bool paged) {
+// Argument codes shared by every decode launcher (0 = arguments usable).
+int check_launch_args(const void* q_lat, const void* q_pe, const void* kv, const void* o_lat, const void* seq_lens,
+                      const void* kv_indices, const void* kv_indptr, int B, int H, int S_fixed, int q_len,
+                      int lat_dim, int rope_dim, bool paged) {
   if (lat_dim != kLat || rope_dim != kRope) return -2;
   if (H < 1 || H > kMaxHeads) return -3;
   if (q_len < 1 || q_len > kMaxQLen || B < 1) return -4;
@@ -872,6 +872,16 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   if (!q_lat || !q_pe || !kv || !o_lat) return -6;
   if (paged && (!seq_lens || !kv_indices || !kv_indptr)) return -6;
   if (!paged && S_fixed < 1) return -7;
+  return 0;
+}
+
+int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, const void* seq_lens,
+           const void* rows, const void* kv_indices, const void* kv_indptr, int B, int H, int S_fixed, int parts,
+           int q_len, int lat_dim, int rope_dim, float scale, float kv_scale, void* workspace, void* stream,
+           bool paged) {
+  const int arg_rc = check_launch_args(q_lat, q_pe, kv, o_lat, seq_lens, kv_indices, kv_indptr, B, H, S_fixed, q_len,
+                                       lat_dim, rope_dim, paged);
+  if (arg_rc != 0) return arg_rc;
   Params p{};
   p.q_lat = static_cast<const uint16_t*>(q_lat);
   p.q_pe = static_cast<const uint16_t*>(q_pe);
@@ -996,7 +1006,10 @@ int launch_mla_decode_a16w8_paged_dev_noalloc(const void* q_lat, const void* q_p
                                               size_t kv_bytes, int q_len) {
   (void)scale_p;
   (void)kv_bytes;
-  if (B < 1 || B > kMaxPagedB || H < 1 || H > kMaxHeads || q_len < 1 || q_len > kMaxQLen) return -4;
+  // The workspace launcher's argument codes first, then the scratch limit.
+  const int arg_rc = check_launch_args(q_lat, q_pe, kv_pool, o_lat, seq_lens, kv_indices, kv_indptr, B, H, 0, q_len,
+                                       lat_dim, rope_dim, true);
+  if (arg_rc != 0) return arg_rc;
   const int eff = clamp_parts(parts, B, H, q_len, true);
   void* ws = nullptr;
   if (eff > 1) {

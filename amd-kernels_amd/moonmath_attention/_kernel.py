@@ -181,13 +181,15 @@ def forward_lite(
     csrc/attention_api.cpp:283-440 (GPU tensors only). ``read_list`` /
     ``write_list`` are int16 [B, H, qtiles, ktiles+2] run-length rows (qtiles =
     ceil(Sq/256), ktiles = ceil(Skv/64)): ``read_list`` names the blocks this
-    step computes, the kernel writes the next step's list into ``write_list``
-    (a block is kept when some q row of the tile came within ``threshold``
-    (log2, < 0) of its running max; the first processed block always). ``phase``
-    1 walks ranges ascending, 0 descending. ``must_do_list`` (int16
-    [len, s0, e0, ...], end exclusive) pins processed blocks as kept.
+    step loads, the kernel writes the next step's list into ``write_list``.
+    Each wave of 32 q rows keeps a listed block for its rows when some valid
+    row's block max came within ``threshold`` (log2) of the row's running max
+    over the blocks the wave kept before (the first processed block always);
+    a block the wave drops adds nothing to its rows. A block stays in the next
+    list when some wave kept it. ``phase`` 1 walks ranges ascending, 0
+    descending. ``must_do_list`` (int16 [len, s0, e0, ...], end exclusive)
+    pins processed blocks as kept in the next list.
     MOONMATH_LITE_PLAIN=1 disables the LPT (heaviest-first) CTA order.
-    With a compute-all read list the output is attention over every key.
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor):

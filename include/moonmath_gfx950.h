@@ -7,7 +7,10 @@
  *  - launches go on the caller's hipStream_t, passed as void*; no host sync;
  *  - return 0 on success, a positive (attention) or negative (MLA) argument
  *    code, otherwise the hipGetLastError() value of the launch;
- *  - stateless and reentrant: no host statics, no symbol uploads.
+ *  - stateless and reentrant (no host statics, no symbol uploads), except
+ *    launch_mla_decode_a16w8_paged_dev_noalloc: it caches one device address
+ *    per GPU and shares a library-owned device scratch array between its
+ *    calls, which callers must serialise per GPU.
  *
  * Each declaration cites the reference interface it replaces
  * (moonmath-ai/amd-kernels, path:line).

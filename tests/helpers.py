@@ -97,14 +97,24 @@ def check_fractions(stats, min_exact=MIN_EXACT, min_strict=MIN_STRICT):
         assert stats["strict_le1"] >= min_strict, f"too many elements beyond strict 1 ULP: {stats}"
 
 
-def aggregate_stats(stats):
-    """Element-weighted totals of several compare_bf16 stats dicts."""
+def aggregate_stats(stats, names=None):
+    """Element-weighted totals of several compare_bf16 stats dicts (one per
+    head, request or tile), plus the worst unit's fractions and the names
+    (or indices) of the units of >= 1000 elements below the per-case bars
+    (exact 0.99, strict 0.999), so a unit that only passes in aggregate is
+    named in the parity log."""
     n = sum(s["n"] for s in stats)
+    names = [str(i) for i in range(len(stats))] if names is None else [str(x) for x in names]
+    big = [(nm, s) for nm, s in zip(names, stats) if s["n"] >= 1000]
     agg = {
         "n": n,
         "exact": sum(s["exact"] * s["n"] for s in stats) / max(n, 1),
         "strict_le1": sum(s["strict_le1"] * s["n"] for s in stats) / max(n, 1),
         "strict_max": max(s["strict_max"] for s in stats),
+        "units": len(stats),
+        "unit_min_exact": min((s["exact"] for _, s in big), default=1.0),
+        "unit_min_strict": min((s["strict_le1"] for _, s in big), default=1.0),
+        "units_below": [nm for nm, s in big if s["exact"] < MIN_EXACT or s["strict_le1"] < MIN_STRICT],
     }
     if all("rule_max" in s for s in stats):
         agg["rule_max"] = max(s["rule_max"] for s in stats)
@@ -150,3 +160,47 @@ def compare_bf16(got, ref, scale=None, tie=None, floor_rel=FLOOR_REL, min_exact=
     if fractions:
         check_fractions(stats, min_exact, min_strict)
     return stats
+
+
+def reference_pattern(name, B, S, H, D=128):
+    """The reference benchmark's synthetic patterns (benchmark/runner.py:48-75),
+    BSHD bf16, the same in every (b, h): "ones" (all ones), "linear" (q = s/S +
+    0.1 d/D, k = s/S, v = s/S + d/D) and "diag" (q = k = one-hot rows of the
+    identity repeated along S, v = s/S in every dim)."""
+    s_idx = (torch.arange(S, dtype=torch.float32) / S).view(S, 1)
+    d_idx = (torch.arange(D, dtype=torch.float32) / D).view(1, D)
+    if name == "ones":
+        q = k = v = torch.ones(S, D)
+    elif name == "linear":
+        q, k, v = s_idx + 0.1 * d_idx, s_idx.expand(S, D), s_idx + d_idx
+    elif name == "diag":
+        q = k = torch.eye(D).repeat(S // D + 1, 1)[:S]
+        v = s_idx.expand(S, D)
+    else:
+        raise ValueError(name)
+    return tuple(t.to(torch.bfloat16).reshape(1, S, 1, D).expand(B, S, H, D).contiguous() for t in (q, k, v))
+
+
+def ones_closed_form(mode):
+    """Every score is 128, so every p is the same p1 = exp2(fl32(128 c) - 17)
+    (m = ceil(fl32(128 c)) = 17) and every output element is
+    mode(S bf16(p1) / (S p1)) = mode(bf16(p1) / p1): the mean of V (1) scaled
+    by the reference's numerics (bf16 P in the numerator, fp32 p in the
+    denominator, attention_kernel.hip:438-451). The quotient is kept away from
+    a bf16 rounding boundary (asserted), so fp32 sums of S equal terms cannot
+    change its rounding."""
+    from oracle import attention as oa
+    from oracle import bf16 as ob
+
+    c = np.float32(oa.SCALE_LOG2E)
+    x = np.float32(np.float64(128.0) * np.float64(c) - 17.0)
+    assert np.ceil(np.float32(128.0) * c) == 17
+    p1 = np.float32(np.exp2(np.float64(x)))
+    mc = ob.MODES[mode]
+    P1 = ob.round_f32(np.array([p1], np.float32), mc)[0]
+    ratio = np.float64(P1) / np.float64(p1)
+    lo = ob.bf16_to_f32(ob.round_bits(np.array([ratio], np.float32), ob.RTZ))[0]
+    ulp = float(ob.ulp_bf16(np.array([ratio]))[0])
+    frac = (ratio - lo) / ulp
+    assert 0.05 < frac < 0.45 or 0.55 < frac < 0.95, frac
+    return int(ob.round_bits(np.array([ratio], np.float32), mc, canon=True)[0])

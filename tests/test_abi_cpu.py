@@ -92,6 +92,23 @@ def test_mla_launcher_argument_codes():
     assert lib.mla_decode_a16w8_plan_parts_q(4, 1024, 9, 16) == -4
 
 
+def test_mla_noalloc_argument_codes_match_the_workspace_launcher():
+    """The allocation-free entry returns the workspace launcher's code for every
+    argument error, checked before its own scratch limit (-9): bad dims -2,
+    bad H -3, bad q_len or B -4, null pointers -6 -- also with a parts count
+    whose records would not fit the scratch array."""
+    lib = _lib.lib
+    nul = None
+    args = (nul, nul, nul, nul, nul, nul, nul, nul)
+    for B, H, parts, lat, ql in ((1, 16, 1, 256, 1), (1, 129, 1, 512, 1), (1, 0, 1, 512, 1), (1, 16, 1, 512, 9),
+                                 (0, 16, 1, 512, 1), (1, 16, 1, 512, 1), (64, 200, 4, 512, 2), (64, 128, 4, 256, 2),
+                                 (64, 128, 4, 512, 2)):
+        want = lib.launch_mla_decode_a16w8_paged_dev(*args, B, H, parts, lat, 64, 1.0, 1.0, 1.0, nul, nul, 0, ql)
+        got = lib.launch_mla_decode_a16w8_paged_dev_noalloc(*args, B, H, parts, lat, 64, 1.0, 1.0, 1.0, nul, 0, ql)
+        assert got == want != 0, (B, H, parts, lat, ql, got, want)
+    assert lib.launch_mla_decode_a16w8_paged_dev_noalloc(*args, 1, 129, 1, 512, 64, 1.0, 1.0, 1.0, nul, 0, 1) == -3
+
+
 def test_mla_planners():
     for B, H, S, ql in [(64, 128, 8192, 1), (64, 128, 8192, 2), (64, 16, 8192, 1), (2, 16, 2048, 4), (1, 1, 1, 1),
                         (8, 100, 4096, 1), (8, 48, 4096, 2)]:

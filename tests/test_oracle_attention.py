@@ -397,3 +397,16 @@ def test_tolerance_rule_rejects_wrong_p_rounding_on_peaked_inputs(out_mode, p_mo
     bad = oa.forward(q, k, v, out_mode, p_mode=p_mode)
     with pytest.raises(AssertionError):
         compare_bf16(bad[0, 0], ref[0, 0], scl[0, 0], tie[0, 0])
+
+
+@pytest.mark.parametrize("mode", ["rtne", "rtna", "rtz"])
+def test_ones_pattern_is_its_closed_form(mode):
+    """The reference benchmark's "ones" inputs (every score 128, V = 1): the
+    oracle's every output equals the hand-derived mode(bf16(p1) / p1), 1.0 in
+    RTNE / RTNA and 0x3F7F in RTZ (truncated P over unrounded p)."""
+    from helpers import ones_closed_form, reference_pattern
+
+    q, k, v = (t[0, :, 0].float().numpy() for t in reference_pattern("ones", 1, 1024, 1))
+    want = ones_closed_form(mode)
+    assert want == (0x3F7F if mode == "rtz" else 0x3F80)
+    assert np.all(oa.head_forward(q, k, v, ob.MODES[mode])[0] == want)

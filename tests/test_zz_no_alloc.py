@@ -2,8 +2,9 @@
 against the launcher it varies (launch_mla_decode_a16w8_paged_dev with a
 caller workspace): bit-identical output on two calls in a row, the second
 with a smaller input (so stale contents of the library's array from the first
-call must not leak into it), and its size limit. All calls go through the C
-ABI."""
+call must not leak into it), its size limit, and its argument codes (those of
+the workspace launcher, checked before the size limit). All calls go through
+the C ABI."""
 import pytest
 import torch
 
@@ -81,4 +82,22 @@ def test_noalloc_rejects_records_beyond_its_array():
         KV_SCALE, 1.0, _lib.stream_ptr(DEV), idx.numel() * 576, q_len)
     torch.cuda.synchronize()
     assert rc == -9
+    assert torch.all(o == 7.0)
+
+
+def test_noalloc_argument_codes_before_the_size_limit():
+    """Bad H gives the workspace launcher's -3 (not the size code), also with
+    parts whose records would not fit; bad dims -2; nothing is launched."""
+    B, q_len, parts = 64, 2, 4
+    t, _ = _inputs(B, 16, q_len, 100, 300, seed=340)
+    q_lat, q_pe, pool, lens, idx, indptr = t
+    o = torch.full((B, q_len, 16, 512), 7.0, dtype=torch.bfloat16, device=DEV)
+    p = _lib.ptr
+    st = _lib.stream_ptr(DEV)
+    for H, lat, want in ((200, 512, -3), (0, 512, -3), (128, 256, -2)):
+        rc = _lib.lib.launch_mla_decode_a16w8_paged_dev_noalloc(
+            p(q_lat), p(q_pe), p(pool), p(o), p(lens), None, p(idx), p(indptr), B, H, parts, lat, 64, SCALE_192,
+            KV_SCALE, 1.0, st, idx.numel() * 576, q_len)
+        assert rc == want, (H, lat, rc)
+    torch.cuda.synchronize()
     assert torch.all(o == 7.0)
