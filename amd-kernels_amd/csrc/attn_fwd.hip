@@ -572,14 +572,18 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // to its rows: no PV MFMAs (its deferred tail included), no l, no max
       // change. The wave's bit in the block's LDS vote byte feeds the next
       // step's list.
+      // A lane holds half of its row's scores. With c > 0, rounding to fp32 is
+      // monotone, so fl(fl(max(a, b) c) - run) > threshold holds exactly when it
+      // holds for a or for b: each lane tests its own half, and the row's full
+      // max (for run_mx) is formed off the critical path, after the PV.
       bool wkeep = true;
+      float bmh = 0.f;
       if constexpr (LITE) {
 #pragma clang fp contract(off)
-        const float bm = xor32_max(vmx) * c;
-        const bool keep = row_valid && (bm - run_mx > p.threshold);
+        bmh = vmx * c;
+        const bool keep = row_valid && (bmh - run_mx > p.threshold);
         wkeep = __builtin_amdgcn_ballot_w64(keep) != 0 || i == 0;
         if (wkeep) {
-          run_mx = fmaxf(run_mx, bm);
           if (lane == 0) {
             // Inline asm: the compiler would put a vmcnt(0) wait (for the
             // in-flight K/V DMAs, which also write LDS) before an atomic it
@@ -626,6 +630,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
         ptail = pf[1][1];
         row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
+        if constexpr (LITE) run_mx = fmaxf(run_mx, xor32_max(bmh));
       }
     };
     for (int i = 0; i < nblk; i += 2) {

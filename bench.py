@@ -7,7 +7,14 @@ in HBM; one step = one ``moonmath_attention.forward`` call (V transpose +
 forward kernel, as the reference times it, benchmark/runner.py:176-181).
 
 ``roofline`` is for the dominant kernel (the attention forward kernel alone,
-timed with HIP events on the stream it is launched on). ``cpu_baseline`` times
+timed with HIP events on the stream it is launched on); its ``traffic`` (HBM
+bytes per launch) comes from two rocprofv3 counter passes (FETCH_SIZE, then
+WRITE_SIZE, each scaled by what the counter reads for a 1 GiB device copy)
+that bench.py runs over this same build in child processes (``traffic_pass``
+says how; ``--no-traffic`` skips them and falls back to the committed profile
+figure). ``passes`` keys give the median of 5 further timing passes beside the
+mean (the reference reports medians of 5 passes, benchmark/bench_table.py:50-55).
+``cpu_baseline`` times
 the reference repo's CPU oracle formula (examples/basic.py:16-17) over the
 whole headline workload on this host's cores (median of 3). Extra keys:
 ``attention`` (the configs[0] tiny case, every round mode, the reference
@@ -15,14 +22,20 @@ benchmark's "realistic" inputs, the configs[3] long shapes, a shape whose tail
 KV-split fires, with and without the split, the configs[2] cross-attention
 shapes; each leg other than the headline's modes carries a ``cpu`` figure of
 the same formula on its own input bits, the whole leg or a stated subset of
-heads and rows), ``lite`` and ``mla`` (configs[4] decode lines with their own
-CPU baseline, the reference test's fp32 formula).
+heads and rows; and the reference's other published shapes, README.md:96-124,
+as RTNE legs beside its MI300X times), ``lite`` and ``mla`` (configs[4] decode
+lines with their own CPU baseline, the reference test's fp32 formula).
 """
 import argparse
+import glob
 import json
 import os
 import pathlib
+import shutil
+import signal
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = pathlib.Path(__file__).resolve().parent
@@ -73,6 +86,14 @@ def _time(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def _passes(torch, fn, iters, passes=5):
+    """Per-pass mean ms of `passes` further timing passes of `iters` calls each
+    (no warmup between them: the caller has just timed fn), and their median."""
+    ms = sorted(_time(torch, fn, iters, 0) for _ in range(passes))
+    return {"median_ms": round(ms[len(ms) // 2], 4), "passes": len(ms), "iters": iters,
+            "min_ms": round(ms[0], 4), "max_ms": round(ms[-1], 4)}
+
+
 def _headline_inputs(torch):
     """configs[1] inputs, N(0,1) bf16 drawn on the CPU from seed 42 (the CPU
     baseline runs on the same bits)."""
@@ -91,6 +112,7 @@ def bench_attention(args, torch, ma, _lib, qkv_cpu):
     ms = _time(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.steps,
                args.warmup)
     wall = time.perf_counter() - t0
+    med = _passes(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.steps)
 
     # Dominant kernel alone: forward kernel over a pre-transposed V_t, events on
     # the launch stream (torch's current stream, passed to the C ABI).
@@ -104,14 +126,21 @@ def bench_attention(args, torch, ma, _lib, qkv_cpu):
                                                 128, 1, None, sp)), max(args.steps, 5), 2)
     assert set(rcs) == {0}, set(rcs)
     achieved = flops / (kms * 1e-3) / 1e12
-    traffic = None
-    tfile = ROOT / "profiles" / "attn_fwd_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    # No nested counter passes from a leg run or from inside a profiler.
+    under_prof = any(k.startswith("ROCPROF") for k in os.environ)
+    tpass = None if (args.no_traffic or args.only or under_prof) else measure_traffic(mode)
+    traffic = tpass.get("hbm_bytes_per_launch") if tpass else None
+    if traffic is None:
+        tfile = ROOT / "profiles" / "attn_fwd_traffic.json"
+        if tfile.exists():
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+            tpass = dict(tpass or {}, source=str(tfile.relative_to(ROOT)), measured=False)
     return {
         "ms": ms,
         "value": flops / (ms * 1e-3) / 1e12,
         "wall_s": wall,
+        "passes": med,
+        "traffic_pass": tpass,
         "kernel_ms": kms,
         "roofline": {
             "bound": "mfma",
@@ -124,12 +153,111 @@ def bench_attention(args, torch, ma, _lib, qkv_cpu):
     }
 
 
-# The reference's published MI300X times (README.md:98-121), other hardware:
+def run_traffic_workload(torch, _lib, mode):
+    """The workload of a counter pass (``--only traffic``): three 1 GiB device
+    copies (the counters' calibration: 1048576 KiB read and written each), then
+    four launches of the headline forward kernel over a pre-transposed V_t."""
+    n = 1 << 30
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    B, S, H = 2, 8192, 24
+    q, k, v = (t.to("cuda:0") for t in _headline_inputs(torch))
+    out = torch.empty_like(q)
+    vt = torch.empty(_lib.lib.moonmath_attention_vt_bytes(B, H, S) // 2, dtype=torch.bfloat16, device="cuda:0")
+    sp = _lib.stream_ptr(q.device)
+    assert getattr(_lib.lib, f"launch_v_transpose_{mode}")(_lib.ptr(v), _lib.ptr(vt), B * H * S, S, H, 1, sp) == 0
+    fwd = getattr(_lib.lib, f"launch_attention_forward_{mode}")
+    for _ in range(4):
+        assert fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(vt), _lib.ptr(out), B, H, S, S, 128, 1, None, sp) == 0
+    torch.cuda.synchronize()
+    _log("bench: traffic workload done")
+
+
+def _counter_pass(counter, mode, timeout_s=180):
+    """Per-dispatch values of `counter` (KiB) for the copy kernel and the
+    attention forward kernel, from one rocprofv3 pass over ``--only traffic``;
+    the first dispatch of each kernel is dropped. None when rocprofv3 is absent
+    or the pass fails."""
+    rp = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(rp):
+        return None, "rocprofv3 not found"
+    out = tempfile.mkdtemp(prefix="mm_traffic_")
+    cmd = [rp, "--kernel-trace", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "c", "--",
+           sys.executable, str(pathlib.Path(__file__).resolve()), "--only", "traffic", "--mode", mode]
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, env=env,
+                                start_new_session=True)
+        try:
+            _, err = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.communicate()
+            return None, f"{counter} pass timed out after {timeout_s} s"
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            tail = err.decode(errors="replace").strip().splitlines()[-3:]
+            return None, f"{counter} pass wrote no counters (rc {proc.returncode}): {' | '.join(tail)}"
+        import csv
+
+        vals = {}
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] != counter:
+                    continue
+                name = row["Kernel_Name"]
+                key = "copy" if "copyBuffer" in name else ("attn" if "attn_fwd_kernel" in name else None)
+                if key:
+                    vals.setdefault(key, []).append(float(row["Counter_Value"]))
+        if "copy" not in vals or "attn" not in vals:
+            return None, f"{counter} pass: kernels missing from the counters ({sorted(vals)})"
+        avg = {k: sum(v[1:]) / len(v[1:]) if len(v) > 1 else v[0] for k, v in vals.items()}
+        avg["dispatches"] = {k: len(v) for k, v in vals.items()}
+        return avg, None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def measure_traffic(mode):
+    """HBM bytes per launch of the headline forward kernel, measured now on
+    this build: FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each times its
+    scale, 1048576 KiB over what the counter reads for the 1 GiB copy (FETCH
+    2.000, WRITE 1.000 on MI355X)."""
+    res = {"measured": True, "counters": "rocprofv3 --kernel-trace --pmc FETCH_SIZE | WRITE_SIZE, one pass each",
+           "workload": "bench.py --only traffic (3 x 1 GiB copy, 4 x forward kernel)"}
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        avg, err = _counter_pass(counter, mode)
+        if avg is None:
+            _log(f"bench: traffic pass unavailable: {err}")
+            return {"measured": False, "error": err}
+        factor = avg["copy"] / 1048576.0
+        got[counter] = {"kib_per_dispatch": round(avg["attn"], 1), "copy_kib": round(avg["copy"], 1),
+                        "scale": round(1.0 / factor, 4), "bytes": avg["attn"] * 1024.0 / factor,
+                        "dispatches": avg["dispatches"]}
+    total = got["FETCH_SIZE"]["bytes"] + got["WRITE_SIZE"]["bytes"]
+    alg = 4 * 2 * 8192 * 24 * 128 * 2  # Q, K, V_t read + O written, bf16
+    res.update(fetch=got["FETCH_SIZE"], write=got["WRITE_SIZE"], hbm_bytes_per_launch=int(round(total)),
+               algorithmic_bytes=alg, ratio=round(total / alg, 4))
+    _log(f"bench: traffic {total / 2**20:.1f} MiB per launch ({total / alg:.3f}x algorithmic)")
+    return res
+
+
+# The reference's published MI300X times (README.md:96-124), other hardware:
 # context for the extra legs, not a baseline of this metric.
 REF_MI300X_MS = {
     ("headline", "rtne"): 3.083, ("headline", "rtna"): 3.022, ("headline", "rtz"): 2.983,
     ("1x32x16384", "rtne"): 8.013, ("2x8x86016", "rtne"): 101.071,
+    ("2x24x16384", "rtne"): 11.670, ("4x16x16384", "rtne"): 15.591, ("1x64x16384", "rtne"): 15.528,
+    ("2x24x32768", "rtne"): 46.002, ("2x16x65536", "rtne"): 117.612, ("1x16x131072", "rtne"): 232.517,
 }
+# Shapes (B, H, S) of the reference's table not benched elsewhere in this file.
+PUBLISHED_SHAPES = ((2, 24, 16384), (4, 16, 16384), (1, 64, 16384), (2, 24, 32768), (2, 16, 65536),
+                    (1, 16, 131072))
 
 
 def _leg(name, B, H, Sq, Skv, ms, **extra):
@@ -163,10 +291,11 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
     q, k, v = (t.to("cuda:0") for t in qkv_cpu)
     out = torch.empty_like(q)
     for mode in ("rtne", "rtna", "rtz"):
-        ms = _time(torch, lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"), args.steps,
-                   args.warmup)
+        fn = (lambda i: ma.forward(q, k, v, out=out, round_mode=mode, layout="bshd"))
+        ms = _time(torch, fn, args.steps, args.warmup)
         res[f"headline_{mode}"] = _leg(f"headline {mode}", 2, 24, 8192, 8192, ms, round_mode=mode,
-                                       ref_mi300x_ms=REF_MI300X_MS[("headline", mode)])
+                                       ref_mi300x_ms=REF_MI300X_MS[("headline", mode)],
+                                       median5=_passes(torch, fn, args.steps))
     qr, kr, vr = (t.to("cuda:0") for t in realistic_bf16(2, 8192, 24, seed=42))
     ms = _time(torch, lambda i: ma.forward(qr, kr, vr, out=out, round_mode="rtne", layout="bshd"), args.steps,
                args.warmup)
@@ -188,6 +317,26 @@ def bench_attention_extra(args, torch, ma, qkv_cpu):
             res[f"long_{key}_rtne"]["cpu"] = cpu_attention(
                 torch, q[:1, :rows, :1].cpu(), k[:1, :, :1].cpu(), v[:1, :, :1].cpu())
             res[f"long_{key}_rtne"]["cpu"]["sample"] = f"1 of {B * H} heads x {rows} of {S} q rows"
+        del q, k, v, o
+    # The reference's other published shapes (README.md:96-124), RTNE: the mean
+    # of a timed region, then the median of 5 passes (about 0.3 s each) as the
+    # reference reports; CPU on one head's first 2048 q rows.
+    for B, H, S in PUBLISHED_SHAPES:
+        g.manual_seed(71)
+        q, k, v = (torch.randn(B, S, H, 128, generator=g, device="cuda:0").to(torch.bfloat16) for _ in range(3))
+        o = torch.empty_like(q)
+        fn = (lambda i: ma.forward(q, k, v, out=o, round_mode="rtne", layout="bshd"))
+        est_ms = attention_flops(B, H, S, S) / 1.1e12 * 1e3
+        iters = max(2, min(args.steps, int(300 / est_ms)))
+        ms = _time(torch, fn, iters, 2)
+        key = f"{B}x{H}x{S}"
+        res[f"published_{key}_rtne"] = _leg(f"published {key} rtne", B, H, S, S, ms, round_mode="rtne",
+                                            ref_mi300x_ms=REF_MI300X_MS[(key, "rtne")],
+                                            median5=_passes(torch, fn, iters))
+        if cpu:
+            res[f"published_{key}_rtne"]["cpu"] = cpu_attention(
+                torch, q[:1, :2048, :1].cpu(), k[:1, :, :1].cpu(), v[:1, :, :1].cpu())
+            res[f"published_{key}_rtne"]["cpu"]["sample"] = f"1 of {B * H} heads x 2048 of {S} q rows"
         del q, k, v, o
     # A shape whose last round of CTAs the tail planner splits: 17 q-blocks x 48
     # heads = 816 CTAs = 3 rounds of 256 + a 48-CTA tail.
@@ -312,6 +461,7 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1)), c
                                               parts, SCALE_192, KV_SCALE)
 
         us = _time(torch, call, steps, warmup) * 1e3
+        med = _passes(torch, call, steps)
         # Algorithmic bytes: KV once + Q in + O out + block tables and lengths.
         nbytes = sum_l * 576 + B * q_len * H * (576 + 512) * 2 + 4 * (n_blocks + B)
         flops = 2.0 * (576 + 512) * H * q_len * sum_l
@@ -321,9 +471,10 @@ def bench_mla(torch, ma, steps, warmup, configs=((128, 1), (128, 2), (16, 1)), c
             "B": B, "H": H, "q_len": q_len, "parts": parts, "us": round(us, 2),
             "hbm_GBs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
             "mfma_TFLOPs": round(tfs, 1), "pct_bf16_peak": round(100 * tfs / PEAK_BF16_TFLOPS, 2),
-            "bytes": nbytes,
+            "bytes": nbytes, "median5_us": round(med["median_ms"] * 1e3, 2),
         }
-        _log(f"bench: mla H={H} q_len={q_len}: {us:.1f} us, {gbs:.0f} GB/s, {tfs:.0f} TFLOP/s")
+        _log(f"bench: mla H={H} q_len={q_len}: {us:.1f} us (median of 5 passes {med['median_ms'] * 1e3:.1f}), "
+             f"{gbs:.0f} GB/s, {tfs:.0f} TFLOP/s")
         if cpu:
             rec["cpu_baseline"] = mla_cpu_baseline(torch, qs_cpu[0], cpu_sets[0], lens, nbytes, flops)
         results.append(rec)
@@ -461,9 +612,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mla", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra attention legs")
-    ap.add_argument("--only", choices=["attention", "mla", "copy"], default=None,
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 counter passes behind roofline.traffic")
+    ap.add_argument("--only", choices=["attention", "mla", "copy", "traffic"], default=None,
                     help="run one leg only (for rocprofv3 counter passes); 'copy' runs a plain "
-                         "1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE")
+                         "1 GiB device copy used to calibrate FETCH_SIZE / WRITE_SIZE; 'traffic' "
+                         "the workload of bench.py's own counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -485,6 +639,9 @@ def main():
         torch.cuda.synchronize()
         _log(f"bench: copied {n} bytes x3 (calibration)")
         return
+    if args.only == "traffic":
+        run_traffic_workload(torch, _lib, args.mode)
+        return
     if args.only == "mla":
         print(json.dumps(bench_mla(torch, ma, args.steps, args.warmup, cpu=False)), flush=True)
         return
@@ -493,7 +650,8 @@ def main():
     att = bench_attention(args, torch, ma, _lib, qkv_cpu)
     _log(f"bench: attention {att['value']:.1f} TFLOP/s, kernel {att['kernel_ms']:.3f} ms")
     if args.only == "attention":
-        print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"]}), flush=True)
+        print(json.dumps({"attention_tflops": att["value"], "kernel_ms": att["kernel_ms"],
+                          "traffic": att["roofline"]["traffic"]}), flush=True)
         return
     extra = None if args.no_extra else bench_attention_extra(args, torch, ma, qkv_cpu)
     lite = None if args.no_extra else bench_lite(args, torch, ma, qkv_cpu)
@@ -525,6 +683,8 @@ def main():
         },
         "roofline": att["roofline"],
         "cpu_baseline": cpu,
+        "passes": att["passes"],
+        "traffic_pass": att["traffic_pass"],
     }
     if extra is not None:
         line["attention"] = extra
