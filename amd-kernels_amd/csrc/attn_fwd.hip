@@ -722,40 +722,62 @@ __global__ __launch_bounds__(kThreads, 1) void attn_lite_kernel(Params p) {
 // LPT order of the lite CTAs (reference plan_lite_order, :1296-1347): CTAs
 // sorted by the number of blocks their read-list row keeps, heaviest first, in
 // 64 buckets of kept/(nkb+1); a stable counting sort (thread t owns the
-// contiguous CTA range [t*C, (t+1)*C)), so the order is deterministic. One
-// CTA of 256 threads; up to kLptMaxCtas CTAs.
+// contiguous CTA range [t*C, (t+1)*C)), so the order is deterministic. Two
+// launches: lite_count_kernel buckets the rows, one thread per row over many
+// CUs (a row's entries are scattered relative to its neighbours', so one CU
+// doing every row is bound by its memory pipeline's rate of distinct cache
+// lines: ~36 us at 1536 rows of ~25 ranges, against ~3 us spread out); then
+// lite_order_kernel (one CTA of 256 threads) sorts the buckets, up to
+// kLptMaxCtas CTAs. Workspace: the order (int per CTA), then the buckets
+// (byte per CTA).
 // ---------------------------------------------------------------------------
 constexpr int kLptThreads = 256;
+constexpr int kLptCountThreads = 64;  // rows per counting CTA
 constexpr int kLptBuckets = 64;
 constexpr int kLptMaxCtas = 65536;
+constexpr int kLptPairBatch = 16;     // pairs whose entries are loaded together
 
-// Kept blocks of a read-list row: the sum of |end - start| over its pairs
-// (row[i], row[i - 1]), i = len, len - 2, ... >= 2. The length and the next
-// kLptHead - 1 entries are loaded together (rows of up to 4 pairs cost one
-// round of latency); later entries one by one. Reads stay inside the row.
-constexpr int kLptHead = 9;
-__device__ __forceinline__ void lite_row_head(const int16_t* row, int nkb, int (&e)[kLptHead]) {
-#pragma unroll
-  for (int j = 0; j < kLptHead; ++j) e[j] = row[j <= nkb + 1 ? j : nkb + 1];
-}
-__device__ __forceinline__ int lite_kept(const int16_t* row, int nkb, const int (&e)[kLptHead]) {
-  int len = e[0];
+// Kept blocks of a read-list row: the sum of |row[i] - row[i - 1]| over
+// i = len, len - 2, ... >= 2, len = row[0] clamped to [0, nkb + 1]. The two
+// entries of kLptPairBatch pairs are loaded before any is used, so a row of
+// up to 16 ranges costs one round of memory latency. Reads stay inside the
+// row. The sum stays below 2^28 ((nkb + 1) / 2 <= 4096 pairs of int16 ids).
+__device__ __forceinline__ int lite_kept(const int16_t* row, int nkb) {
+  int len = row[0];
   len = len < 0 ? 0 : (len > nkb + 1 ? nkb + 1 : len);
   int kept = 0;
+  for (int i0 = len; i0 >= 2; i0 -= 2 * kLptPairBatch) {
+    int hi[kLptPairBatch], lo[kLptPairBatch];
 #pragma unroll
-  for (int i = 2; i < kLptHead; ++i) {
-    const int d = e[i] - e[i - 1];
-    kept += (i <= len && ((len - i) & 1) == 0) ? (d < 0 ? -d : d) : 0;
-  }
-  for (int i = len; i >= kLptHead; i -= 2) {
-    const int d = (int)row[i] - (int)row[i - 1];
-    kept += d < 0 ? -d : d;
+    for (int k = 0; k < kLptPairBatch; ++k) {
+      const int i = i0 - 2 * k;
+      hi[k] = i >= 2 ? (int)row[i] : 0;
+      lo[k] = i >= 2 ? (int)row[i - 1] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kLptPairBatch; ++k) {
+      const int d = hi[k] - lo[k];
+      kept += d < 0 ? -d : d;
+    }
   }
   return kept;
 }
 
-__global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const int16_t* __restrict__ read_list,
-                                                                int* __restrict__ order, int nctas, int nkb) {
+// Bucket of every CTA's row. A count past nkb lands in the top bucket either
+// way; clamping it first keeps the product in range for any row content.
+__global__ __launch_bounds__(kLptCountThreads) void lite_count_kernel(const int16_t* __restrict__ read_list,
+                                                                     uint8_t* __restrict__ bucket, int nctas,
+                                                                     int nkb) {
+  const int w = blockIdx.x * kLptCountThreads + threadIdx.x;
+  if (w >= nctas) return;
+  int kept = lite_kept(read_list + (long long)w * (nkb + 2), nkb);
+  kept = kept < nkb + 1 ? kept : nkb + 1;
+  const int bk = kept * kLptBuckets / (nkb + 1);
+  bucket[w] = (uint8_t)(bk < kLptBuckets ? bk : kLptBuckets - 1);
+}
+
+__global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const uint8_t* __restrict__ bucket,
+                                                                int* __restrict__ order, int nctas) {
   static_assert(kLptThreads == 256 && kLptBuckets == 64, "4 threads' counts per lane, one bucket per lane");
   __shared__ __attribute__((aligned(16))) int hist[kLptBuckets][kLptThreads];
   __shared__ int bucket_base[kLptBuckets];
@@ -765,30 +787,7 @@ __global__ __launch_bounds__(kLptThreads) void lite_order_kernel(const int16_t* 
   const int w0 = t * chunk;
   const int w1 = w0 + chunk < nctas ? w0 + chunk : nctas;
   for (int b = 0; b < kLptBuckets; ++b) hist[b][t] = 0;
-  // Bucket of every CTA: rows dealt round robin over the threads, the heads of
-  // 4 rows in flight per thread.
-  for (int wb = t; wb < nctas; wb += 4 * kLptThreads) {
-    int e[4][kLptHead];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int w = wb + u * kLptThreads;
-      if (w < nctas) lite_row_head(read_list + (long long)w * (nkb + 2), nkb, e[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int w = wb + u * kLptThreads;
-      if (w < nctas) {
-        // A row's kept count is at most the sum of |end - start| over its
-        // (nkb + 1) / 2 pairs of int16 ids (< 2^28); counts past nkb land in
-        // the top bucket anyway, so clamping first keeps the product in range
-        // for any row content.
-        int kept = lite_kept(read_list + (long long)w * (nkb + 2), nkb, e[u]);
-        kept = kept < nkb + 1 ? kept : nkb + 1;
-        const int bk = kept * kLptBuckets / (nkb + 1);
-        bk_of[w] = (uint8_t)(bk < kLptBuckets ? bk : kLptBuckets - 1);
-      }
-    }
-  }
+  for (int w = t; w < nctas; w += kLptThreads) bk_of[w] = bucket[w];
   __syncthreads();
   for (int w = w0; w < w1; ++w) ++hist[bk_of[w]][t];
   __syncthreads();
@@ -1019,9 +1018,10 @@ int launch_fwd(const void* q, const void* k, const void* v_t, void* out, int bat
 }
 
 // LiteAttention launcher (reference launch_attention_forward_lite,
-// attention_kernel.hip:1599-1681). workspace: lite_workspace_bytes ints for
-// the LPT order (null = plain order); LPT runs when the kv range is long
-// enough to amortise its planning launch (48 blocks, as the reference).
+// attention_kernel.hip:1599-1681). workspace: lite_workspace_bytes bytes for
+// the LPT order and buckets (null = plain order); LPT runs when the kv range
+// is long enough to amortise its planning launches (48 blocks, as the
+// reference).
 constexpr int kLiteMinKvBlocksForLpt = 48;
 
 template <int MODE>
@@ -1059,8 +1059,11 @@ int launch_lite(const void* q, const void* k, const void* v_t, void* out, int ba
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (workspace && p.nkb >= kLiteMinKvBlocksForLpt && total <= kLptMaxCtas) {
     p.order = static_cast<const int*>(workspace);
-    hipLaunchKernelGGL(lite_order_kernel, dim3(1), dim3(kLptThreads), 0, st, p.read_list,
-                       static_cast<int*>(workspace), (int)total, p.nkb);
+    uint8_t* bucket = static_cast<uint8_t*>(workspace) + total * sizeof(int);
+    hipLaunchKernelGGL(lite_count_kernel, dim3((unsigned)((total + kLptCountThreads - 1) / kLptCountThreads)),
+                       dim3(kLptCountThreads), 0, st, p.read_list, bucket, (int)total, p.nkb);
+    hipLaunchKernelGGL(lite_order_kernel, dim3(1), dim3(kLptThreads), 0, st, bucket, static_cast<int*>(workspace),
+                       (int)total);
   }
   hipLaunchKernelGGL((attn_lite_kernel<MODE>), dim3((unsigned)total), dim3(kThreads), 0, st, p);
   const hipError_t e = hipGetLastError();
@@ -1109,7 +1112,7 @@ extern "C" {
   }                                                                                                          \
   size_t lite_workspace_bytes_##NAME(int batch, int heads, int seq_len) {                                    \
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return 0;                                                  \
-    return (size_t)batch * heads * ((seq_len + kRowsPerCta - 1) / kRowsPerCta) * sizeof(int);                \
+    return (size_t)batch * heads * ((seq_len + kRowsPerCta - 1) / kRowsPerCta) * (sizeof(int) + 1);          \
   }
 
 MM_ATTN_MODE_SYMBOLS(rtne, mm::kRTNE)

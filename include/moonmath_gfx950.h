@@ -63,10 +63,13 @@ size_t tail_workspace_bytes_rtz(void);
  * [B,H,ceil(Sq/256),ceil(Skv/64)+2] run-length rows: len, then (end, start)
  * pairs read from the back, walked ascending when phase != 0, descending
  * otherwise) are computed; write_list (same shape) receives the next step's
- * rows: a processed block is kept when some q row of the 256-row tile came
- * within `threshold` (log2) of its running max, when it is the first block
- * processed, or when must_do_list (int16 [len, s0, e0, ...], end exclusive;
- * nullable) holds it. v_t is the output of launch_v_transpose_<mode>.
+ * rows. Each wave of 32 q rows keeps a processed block for its rows when
+ * some valid row's block max came within `threshold` (log2) of the row's
+ * running max over the blocks the wave kept before, or when it is the first
+ * block processed; a block the wave drops adds nothing to its rows. The next
+ * list keeps a block some wave kept, or one that must_do_list (int16 [len,
+ * s0, e0, ...], end exclusive; nullable) holds. v_t is the output of
+ * launch_v_transpose_<mode>.
  * workspace: lite_workspace_bytes_<mode>() bytes for the heaviest-first CTA
  * order, or NULL (plain order). Codes: as the dense launcher, plus 4 (NULL
  * read or write list) and 6 (more than 8192 K-blocks, Skv > 524288).
@@ -84,7 +87,8 @@ int launch_attention_forward_lite_rtz(const void* q, const void* k, const void* 
                                       void* write_list, const void* must_do_list, float threshold, int phase,
                                       int layout, void* workspace, void* stream);
 
-/* Bytes of the lite CTA-order buffer (one int per 256-row q tile and head).
+/* Bytes of the lite CTA-order workspace: per 256-row q tile and head one int
+ * (the order, first) and one byte (its work bucket, after the order).
  * Replaces csrc/attention_kernel.hip:1554-1558. */
 size_t lite_workspace_bytes_rtne(int batch, int heads, int seq_len);
 size_t lite_workspace_bytes_rtna(int batch, int heads, int seq_len);
