@@ -39,6 +39,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "mm_common.hpp"
 
@@ -78,6 +79,24 @@ constexpr int kLiteVoteOff = kLiteListOff + kMaxLiteBlocks * 2;
 constexpr int kLiteMiscOff = kLiteVoteOff + kMaxLiteBlocks;
 constexpr int kLdsLiteBytes = kLiteMiscOff + 64;
 static_assert(kLdsLiteBytes <= 160 * 1024, "lite LDS fits a CU");
+
+// Short KV (at most kShortMaxBlocks blocks per head): persistent CTAs keep the
+// head's K / V_t blocks resident in 2-slot rings and stage the next q-block's
+// Q (256 rows x 256 B) in LDS while computing the current one.
+constexpr int kShortMaxBlocks = 2;
+constexpr int kShortOStageOff = 2 * kShortMaxBlocks * kKBytes;         // 64 KB: output staging
+constexpr int kShortQStageOff = kShortOStageOff + kWaves * 16 * 256;    // 96 KB: Q stage
+constexpr int kShortQStageBytes = kRowsPerCta * kD * 2;                // 64 KB
+constexpr int kLdsShortBytes = kShortQStageOff + kShortQStageBytes;     // 160 KB
+static_assert(kLdsShortBytes <= 160 * 1024, "short-KV LDS fits a CU");
+
+// Item state of a persistent short-KV CTA across run_tile calls.
+struct ShortCtx {
+  int resident;  // (b, h) whose K / V_t blocks are in the slots, or -1
+  int next_bh;   // the next item's (b, h) and q-block, whose Q is prefetched
+  int next_qb;   //   into the stage during this item (next_bh < 0: none)
+  bool first;    // the stage does not hold this item's Q yet
+};
 
 struct Params {
   const uint16_t* q;
@@ -194,9 +213,9 @@ __device__ __forceinline__ void lite_emit(const Params& p, long long row, int n,
 // bf16(P) under the final max times an exact power of two (up to the last
 // fp32 bit of the exp2 argument): the output does not depend on where the
 // rebases happen, on the KV blocking or on the split.
-template <int MODE, bool LITE>
+template <int MODE, bool LITE, bool SHORT = false>
 __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb_begin, int kb_end, int part,
-                                         char* lds) {
+                                         char* lds, ShortCtx* sc = nullptr) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -219,8 +238,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // consecutive 16-byte cells per 16 lanes (conflict free), and the 8 reads of
   // a row tile differ only by the immediate offset 512 * ds.
   // V_t slot: fragments [t(2)][s(2)][dt(4)], 1 KB each in lane order.
+  // Short KV: K slots 0..1, V_t slots 0..1, the output stage, the Q stage.
   char* kring = lds;
-  char* vring = lds + kRing * kKBytes;
+  char* vring = lds + (SHORT ? kShortMaxBlocks : kRing) * kKBytes;
   auto kslot_off = [](int k, int c) { return (k >> 4) * 4096 + c * 256 + (k & 15) * 16; };
   // This lane's MFMA fragment cell for row tile t, k-step ds: kfrag_lane +
   // 8192 t + 512 ds (rows t*32 + r, chunk 2 ds + g), constants the LDS reads
@@ -261,7 +281,37 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
   bf16x8 qf[8];
   const int q_row0 = qb * kRowsPerCta + wave * kQRowsPerTile;
-  {
+  // Short KV: Q staged in LDS, row rr's 16-byte chunk cc at
+  // rr * 256 + 16 * (cc ^ (rr & 15)); wave w's 8 DMAs fill rows 32w .. 32w+31
+  // (instruction i: rows 4i .. 4i+3, lane l -> row 4i + l/16, slot l % 16).
+  char* qstage = lds + kShortQStageOff;
+  auto issue_q_stage = [&](int sbh, int sqb) {
+    const uint16_t* sq = p.q + head_base(sbh / p.H, sbh % p.H, p.Sq, p.H, p.bshd);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int ins = wave * 8 + k;
+      const int rr = 4 * ins + (lane >> 4);
+      const int cc = (lane & 15) ^ (rr & 15);
+      int qr = sqb * kRowsPerCta + rr;
+      qr = qr < p.Sq ? qr : p.Sq - 1;
+      dma16_opaque(sq + (long long)qr * row_stride + cc * 8, qstage + ins * kFragBytes);
+    }
+  };
+  if constexpr (SHORT) {
+    // This item's Q: prefetched during the previous item (each wave waited for
+    // its own DMAs before that item's output stores), or gathered now.
+    if (sc->first) {
+      issue_q_stage(bh, qb);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_barrier" ::: "memory");  // every wave's share of the stage has landed
+    const int rr = wave * kQRowsPerTile + r;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qf[ds] = *reinterpret_cast<const bf16x8*>(qstage + rr * 256 + 16 * ((2 * ds + g) ^ (rr & 15)));
+    // The stage is read and every wave is done with the previous item's blocks.
+    lds_reads_done_barrier();
+  } else {
     int qr = q_row0 + r;
     qr = qr < p.Sq ? qr : p.Sq - 1;
     const uint16_t* src = qh + (long long)qr * row_stride + g * 8;
@@ -394,16 +444,35 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       issue_k(kb, slot);
       issue_v(kb, slot);
     };
-    issue_kv(blk_of(0), 0);
-    if (nblk > 1) issue_kv(blk_of(1), 1);
-    if (nblk > 2) issue_kv(blk_of(2), 2);
-    // 4 DMAs per wave per block: block 0 has landed, blocks 1 and 2 stay in flight.
-    if (nblk > 2) {
-      wait_vmem_barrier<8>();
-    } else if (nblk > 1) {
-      wait_vmem_barrier<4>();
+    if constexpr (SHORT) {
+      // The head's blocks stay in the slots across its q-blocks; then the next
+      // item's Q goes out (8 DMAs per wave), which the block wait leaves in
+      // flight.
+      const bool kv_new = sc->resident != bh;
+      if (kv_new)
+        for (int j = 0; j < nblk; ++j) issue_kv(blk_of(j), j);
+      const bool prefetch = sc->next_bh >= 0;
+      if (prefetch) issue_q_stage(sc->next_bh, sc->next_qb);
+      if (kv_new) {
+        if (prefetch) {
+          wait_vmem_barrier<8>();
+        } else {
+          wait_vmem_barrier<0>();
+        }
+      }
+      sc->resident = bh;
     } else {
-      wait_vmem_barrier<0>();
+      issue_kv(blk_of(0), 0);
+      if (nblk > 1) issue_kv(blk_of(1), 1);
+      if (nblk > 2) issue_kv(blk_of(2), 2);
+      // 4 DMAs per wave per block: block 0 has landed, blocks 1 and 2 stay in flight.
+      if (nblk > 2) {
+        wait_vmem_barrier<8>();
+      } else if (nblk > 1) {
+        wait_vmem_barrier<4>();
+      } else {
+        wait_vmem_barrier<0>();
+      }
     }
     qk(kring, sA);
     mask(sA, blk_of(0));
@@ -420,7 +489,10 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // Block i+1 has landed (block i+2 stays in flight, 4 DMAs per wave); every
       // wave is done with step i-1, so the slot of block i-1 is free.
       sched_fence();
-      if (i + 2 < nblk) {
+      if constexpr (SHORT) {
+        // Every block is resident and no slot is refilled: no barrier, and no
+        // wait for the Q prefetch in flight.
+      } else if (i + 2 < nblk) {
         asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       } else {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -673,20 +745,53 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     return;
   }
 
-  const int qr = q_row0 + r;
-  if (qr >= p.Sq) return;
+  // The wave's 32 output rows go through LDS so that every store instruction
+  // writes whole 256-byte rows (16 lanes per row, 4 rows per instruction):
+  // stored straight from the accumulator layout, each instruction would write
+  // 16 bytes into each of 32 rows' cache lines. Staging: row rr's 16-byte
+  // chunk cc at rr * 256 + 16 * (cc ^ (rr & 15)) (conflict-free writes and
+  // reads). The area is wave-private and idle: dense and lite use K and V_t
+  // ring slots (nblk + 1) % 4 and (nblk + 2) % 4, which the last step neither
+  // reads nor fills (8 KB per wave, all 32 rows at once); the short-KV kernel
+  // its 32 KB output stage (4 KB per wave, 16 rows per round).
   const float inv = (row_l == 0.f) ? 0.f : __builtin_amdgcn_rcpf(row_l);
-  uint16_t* orow = p.out + head_base(b, h, p.Sq, p.H, p.bshd) + (long long)qr * row_stride;
+  uint16_t* ohead = p.out + head_base(b, h, p.Sq, p.H, p.bshd);
+  constexpr int kRoundRows = SHORT ? 16 : kQRowsPerTile;
+  char* ost;
+  if constexpr (SHORT) {
+    ost = lds + kShortOStageOff + wave * (kRoundRows * 256);
+  } else {
+    const int slot = ((wave & 2) ? nblk + 2 : nblk + 1) & (kRing - 1);
+    ost = ((wave & 4) ? vring : kring) + slot * kKBytes + (wave & 1) * (kQRowsPerTile * 256);
+  }
+  u32x2 ow[4][4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int d = dt * 32 + j * 8 + g * 4;
-      u32x2 w;
-      w[0] = pack2_bf16_canon<MODE>(oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv);
-      w[1] = pack2_bf16_canon<MODE>(oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
-      *reinterpret_cast<u32x2*>(orow + d) = w;
+      ow[dt][j][0] = pack2_bf16_canon<MODE>(oacc[dt][4 * j] * inv, oacc[dt][4 * j + 1] * inv);
+      ow[dt][j][1] = pack2_bf16_canon<MODE>(oacc[dt][4 * j + 2] * inv, oacc[dt][4 * j + 3] * inv);
     }
+#pragma unroll
+  for (int rd = 0; rd < kQRowsPerTile / kRoundRows; ++rd) {
+    if (r / kRoundRows == rd) {
+      char* wrow = ost + (r % kRoundRows) * 256 + g * 8;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x2*>(wrow + 16 * ((dt * 4 + j) ^ (r & 15))) = ow[dt][j];
+    }
+#pragma unroll
+    for (int k = 0; k < kRoundRows / 4; ++k) {
+      const int rr = 4 * k + (lane >> 4);  // row within the round
+      const int row = rd * kRoundRows + rr;
+      const int cs = lane & 15;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ost + rr * 256 + 16 * cs);
+      const int orow = q_row0 + row;
+      if (orow < p.Sq)
+        *reinterpret_cast<u32x4*>(ohead + (long long)orow * row_stride + 8 * (cs ^ (row & 15))) = v;
+    }
+  }
 }
 
 template <int MODE>
@@ -704,6 +809,28 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_kernel(Params p) {
     const int kb0 = (int)((long long)p.nkb * j / p.split_ways);
     const int kb1 = (int)((long long)p.nkb * (j + 1) / p.split_ways);
     run_tile<MODE, false>(p, w / p.nqb, w % p.nqb, kb0, kb1, part, lds);
+  }
+}
+
+// Short-KV forward (at most kShortMaxBlocks KV blocks): persistent CTAs, CTA c
+// runs items [c * per_cta, (c + 1) * per_cta) in order (item = (b, h) * nqb +
+// q-block, so consecutive items share a head and its resident blocks). While
+// an item computes, the next item's Q is gathered into the LDS stage and the
+// previous item's output stores drain, so the q-blocks' HBM traffic overlaps
+// the MFMA work instead of alternating with it in lockstep rounds.
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 1) void attn_short_kernel(Params p, int per_cta) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsShortBytes];
+  const int total = p.nqb * p.B * p.H;
+  const int w0 = blockIdx.x * per_cta;
+  const int w1 = w0 + per_cta < total ? w0 + per_cta : total;
+  ShortCtx sc{-1, -1, 0, true};
+  for (int w = w0; w < w1; ++w) {
+    const int wn = w + 1 < w1 ? w + 1 : -1;
+    sc.next_bh = wn >= 0 ? wn / p.nqb : -1;
+    sc.next_qb = wn >= 0 ? wn % p.nqb : 0;
+    run_tile<MODE, false, true>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds, &sc);
+    sc.first = false;
   }
 }
 
@@ -947,6 +1074,14 @@ struct TailPlan {
   int prefix_wgs, tail, split_ways, parts;
 };
 
+// The persistent short-KV kernel serves shapes of at most kShortMaxBlocks KV
+// blocks unless MOONMATH_NO_SHORT_KV is set (a switch for comparing it with
+// the one-CTA-per-q-block kernel on the same shape).
+bool short_kv_enabled() {
+  const char* v = getenv("MOONMATH_NO_SHORT_KV");
+  return !(v && *v && *v != '0');
+}
+
 TailPlan plan_tail(int nqb, int nbh, int nkb, int slots, bool enable, int force_ways) {
   const int wgs = nqb * nbh;
   const TailPlan none{wgs, 0, 1, 0};
@@ -1002,10 +1137,20 @@ int launch_fwd(const void* q, const void* k, const void* v_t, void* out, int bat
   p.scale_log2e = (float)(1.4426950408889634 / 11.313708498984761);
   const long long nbh = (long long)batch * heads;
   if ((long long)p.nqb * nbh > 0x7FFFFFFFLL) return 9;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const long long items = (long long)p.nqb * nbh;
+  if (p.nkb <= kShortMaxBlocks && items > kSlots && force_ways <= 1 && short_kv_enabled()) {
+    // Short KV: one persistent CTA per CU (no tail split: nkb is far below the
+    // planner's minimum).
+    const int per_cta = (int)((items + kSlots - 1) / kSlots);
+    const int grid = (int)((items + per_cta - 1) / per_cta);
+    hipLaunchKernelGGL((attn_short_kernel<MODE>), dim3(grid), dim3(kThreads), 0, st, p, per_cta);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+  }
   const TailPlan tp = plan_tail(p.nqb, (int)nbh, p.nkb, kSlots, workspace != nullptr, force_ways);
   p.prefix_wgs = tp.prefix_wgs;
   p.split_ways = tp.split_ways;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const int grid = tp.prefix_wgs + tp.parts;
   hipLaunchKernelGGL((attn_fwd_kernel<MODE>), dim3(grid), dim3(kThreads), 0, st, p);
   if (tp.parts > 0) {

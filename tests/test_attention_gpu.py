@@ -454,3 +454,26 @@ def test_nan_rows_partial():
     k = k.to(torch.bfloat16)
     out = _forward(q, k, v, "rtne", "bhsd")
     _check(q, k, v, out, "rtne", "bhsd", [(0, 0), (0, 1), (0, 2)], "nan_rows_partial_1x3x300_rtne")
+
+
+# ---- short KV: persistent CTAs with resident K/V and a staged Q ---------------------
+
+@pytest.mark.parametrize("mode", ["rtne", "rtz"])
+@pytest.mark.parametrize("Skv", [1, 64, 77, 128, 129])
+@pytest.mark.parametrize("B,H,Sq,layout", [(2, 24, 4097, "bshd"), (1, 3, 21800, "bhsd")])
+def test_short_kv_persistent_kernel(B, H, Sq, layout, Skv, mode, monkeypatch):
+    """At most 2 KV blocks (Skv <= 128) and more q-blocks than CUs, the
+    persistent short-KV kernel runs (CTAs of 4 or 2 consecutive q-blocks
+    that straddle heads, the ragged last q-block and last KV block; Skv 129
+    is the first shape past it): bit-identical to the one-CTA-per-q-block
+    kernel on the same inputs (each q-block is the same computation), and
+    within the tolerance rule of the oracle on 3 heads."""
+    q, k, v = _make(B, H, Sq, Skv, layout, seed=Sq + Skv, kv_scale=0.5)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    fast = ma.forward(qd, kd, vd, round_mode=mode, layout=layout)
+    monkeypatch.setenv("MOONMATH_NO_SHORT_KV", "1")
+    ref_kernel = ma.forward(qd, kd, vd, round_mode=mode, layout=layout)
+    torch.cuda.synchronize()
+    assert torch.equal(fast.view(torch.int16), ref_kernel.view(torch.int16)), "short-KV kernel differs"
+    heads = [(0, 0), (B - 1, H // 2), (B - 1, H - 1)]
+    _check(q, k, v, fast, mode, layout, heads, f"short_kv_{layout}_{B}x{H}_sq{Sq}_skv{Skv}_{mode}")
