@@ -1049,6 +1049,15 @@ __global__ __launch_bounds__(256) void v_transpose_kernel(const uint16_t* __rest
   }
 }
 
+// Test hook kernel: the output packing of the epilogue and the merge applied
+// to arbitrary fp32 pairs.
+template <int MODE>
+__global__ __launch_bounds__(256) void pack_bf16_kernel(const float* __restrict__ in, uint32_t* __restrict__ out,
+                                                        int npairs) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < npairs) out[i] = pack2_bf16_canon<MODE>(in[2 * i], in[2 * i + 1]);
+}
+
 }  // namespace attn
 }  // namespace mm
 
@@ -1308,6 +1317,25 @@ size_t moonmath_attention_vt_bytes(int batch, int heads, int seq_len_kv) {
   if (batch <= 0 || heads <= 0 || seq_len_kv <= 0) return 0;
   const size_t nkb = (size_t)(seq_len_kv + kKvBlock - 1) / kKvBlock;
   return (size_t)batch * heads * nkb * kVtBlockElems * 2;
+}
+
+int moonmath_pack_bf16(const void* in, void* out, int n, int round_mode, void* stream) {
+  if (!in || !out || n < 0 || (n & 1)) return -6;
+  if (round_mode < 0 || round_mode > 2) return 10;
+  if (n == 0) return 0;
+  const int npairs = n / 2;
+  const dim3 grid((npairs + 255) / 256), block(256);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const float* src = static_cast<const float*>(in);
+  uint32_t* dst = static_cast<uint32_t*>(out);
+  if (round_mode == 0)
+    hipLaunchKernelGGL(pack_bf16_kernel<mm::kRTNE>, grid, block, 0, s, src, dst, npairs);
+  else if (round_mode == 1)
+    hipLaunchKernelGGL(pack_bf16_kernel<mm::kRTNA>, grid, block, 0, s, src, dst, npairs);
+  else
+    hipLaunchKernelGGL(pack_bf16_kernel<mm::kRTZ>, grid, block, 0, s, src, dst, npairs);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : (int)e;
 }
 
 }  // extern "C"

@@ -32,26 +32,6 @@ constexpr float kNegFltMax = -3.402823466e+38f;
 //   RTZ : u (truncate)
 // The "canon" variant maps every NaN to 0x7FFF in all three modes.
 // ---------------------------------------------------------------------------
-template <int MODE>
-__device__ __forceinline__ uint32_t bf16_bits_raw(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if constexpr (MODE == kRTNE) {
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  } else if constexpr (MODE == kRTNA) {
-    return (u + 0x8000u) >> 16;
-  } else {
-    return u >> 16;
-  }
-}
-
-template <int MODE>
-__device__ __forceinline__ uint32_t bf16_bits_canon(float f) {
-  // The NaN test is done on bits so no compiler flag can fold it away.
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  const bool is_nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
-  return is_nan ? kBf16CanonNaN : bf16_bits_raw<MODE>(f);
-}
-
 // Pack two fp32 into one dword of two bf16 (lo = a, hi = b).
 // RTNE uses the gfx950 hardware convert (v_cvt_pk_bf16_f32), which is IEEE
 // round-to-nearest-even and keeps NaN a NaN; RTNA/RTZ use the integer rules.
@@ -74,9 +54,15 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   }
 }
 
+// pack2_bf16 with every NaN mapped to 0x7FFF. A NaN input is first replaced
+// by the fp32 NaN 0x7FFF0000, which each mode's packing turns into 0x7FFF:
+// RTNA's +0x8000 does not carry into bit 16, RTZ truncates, and the RTNE
+// convert returns a NaN input's top half unchanged when its quiet bit is set.
+// Cost: one class test and one select per value, then the plain pack.
 template <int MODE>
 __device__ __forceinline__ uint32_t pack2_bf16_canon(float a, float b) {
-  return bf16_bits_canon<MODE>(a) | (bf16_bits_canon<MODE>(b) << 16);
+  const float canon = __builtin_bit_cast(float, kBf16CanonNaN << 16);
+  return pack2_bf16<MODE>(__builtin_isnan(a) ? canon : a, __builtin_isnan(b) ? canon : b);
 }
 
 // ---------------------------------------------------------------------------

@@ -53,6 +53,7 @@ SIGNATURES.update({
     "mla_decode_a16w8_max_ctas": (_i, []),
     "moonmath_mla_effective_parts": (_i, [_i, _i, _i, _i, _i]),
     "moonmath_fp8e4m3_to_bf16": (_i, [_p, _p, _i, _p]),
+    "moonmath_pack_bf16": (_i, [_p, _p, _i, _i, _p]),
     "launch_mla_kv_quantize": (_i, [_p, _p, _p, _p, ctypes.c_longlong, ctypes.c_longlong, _f, _i, _p]),
 })
 

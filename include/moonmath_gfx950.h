@@ -223,6 +223,12 @@ int launch_mla_kv_quantize(const void* c_kv, const void* k_pe, void* kv_pool, co
  * hardware convert (v_cvt_scalef32_pk_bf16_fp8, scale 1). */
 int moonmath_fp8e4m3_to_bf16(const void* in, void* out, int n, void* stream);
 
+/* Test hook: pack n fp32 values (n even) to bf16 bits with the output packing
+ * of the attention epilogue, the split-KV merge and the MLA outputs
+ * (round_mode 0 RTNE, 1 RTNA, 2 RTZ; every NaN becomes 0x7FFF). The rounding
+ * rules are the reference's bf16_round_one (csrc/attention_kernel.hip:110-145). */
+int moonmath_pack_bf16(const void* in, void* out, int n, int round_mode, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

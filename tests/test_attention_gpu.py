@@ -18,6 +18,7 @@ import torch
 import moonmath_attention as ma
 from moonmath_attention import _lib
 from oracle import attention as oa
+from oracle import bf16 as ob
 from oracle import vt_layout
 from oracle.bf16 import MODES
 from helpers import (aggregate_stats, bits, check_fractions, compare_bf16, f32, growth_log2, log_stats,
@@ -90,6 +91,43 @@ def _forward(q, k, v, mode, layout):
     out = ma.forward(q.to(DEV), k.to(DEV), v.to(DEV), round_mode=mode, layout=layout)
     torch.cuda.synchronize()
     return out
+
+
+def _pack_patterns():
+    """fp32 bit patterns for the output packing: uniform random words plus the
+    classes a rounding rule gets wrong first (zeros, denormals, the lowest
+    normals, ties of both parities, carries into the exponent, overflow to
+    inf, infinities and NaNs of many payloads, both signs)."""
+    rng = np.random.default_rng(20261202)
+    low = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], dtype=np.uint32)
+    tops = np.concatenate([np.arange(0x0000, 0x0100), np.arange(0x7F00, 0x7F81), rng.integers(0, 0x7F80, 512),
+                           [0x3F80, 0x3F81, 0x0080, 0x007F, 0x7F7F]]).astype(np.uint32)
+    grid = ((tops[:, None] << 16) | low[None, :]).ravel()
+    nan = np.concatenate([np.array([0x7F800001, 0x7FBFFFFF, 0x7FC00000, 0x7FFF0000, 0x7FFF7FFF, 0x7FFF8000,
+                                    0x7FFFFFFF], dtype=np.uint32),
+                          rng.integers(0x7F800001, 0x80000000, 4096, dtype=np.uint64).astype(np.uint32)])
+    denorm = rng.integers(1, 0x00800000, 8192, dtype=np.uint64).astype(np.uint32)
+    rand = rng.integers(0, 1 << 32, 1 << 19, dtype=np.uint64).astype(np.uint32)
+    pos = np.concatenate([grid, nan, denorm, [0x7F800000]])
+    u = np.concatenate([pos, pos | np.uint32(0x80000000), rand]).astype(np.uint32)
+    return u if u.size % 2 == 0 else np.append(u, np.uint32(0))
+
+
+@pytest.mark.parametrize("mode", ["rtne", "rtna", "rtz"])
+def test_output_packing_bit_patterns(mode):
+    """The packing every bf16 output goes through, on ~0.6M fp32 patterns: the
+    mode's integer rounding rule on every non-NaN (denormals kept, carries into
+    inf), 0x7FFF for every NaN whatever its sign and payload."""
+    u = _pack_patterns()
+    x = u.view(np.float32)
+    src = torch.from_numpy(x.copy()).to(DEV)
+    out = torch.empty(u.size, dtype=torch.int16, device=DEV)
+    assert _lib.lib.moonmath_pack_bf16(_lib.ptr(src), _lib.ptr(out), u.size, MODES[mode], _lib.stream_ptr(DEV)) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    exp = ob.round_bits(x, MODES[mode], canon=True)
+    bad = np.flatnonzero(got != exp)
+    assert bad.size == 0, [(hex(int(u[i])), hex(int(got[i])), hex(int(exp[i]))) for i in bad[:8]]
 
 
 @pytest.mark.parametrize("mode", ["rtne", "rtna", "rtz"])
