@@ -41,6 +41,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "mm_common.hpp"
 
 namespace mm {
@@ -299,18 +301,19 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   };
   if constexpr (SHORT) {
     // This item's Q: prefetched during the previous item (each wave waited for
-    // its own DMAs before that item's output stores), or gathered now.
+    // its own DMAs before that item's output stores), or gathered now. A wave
+    // gathers and reads only its own 32 rows of the stage, so no barrier:
+    // the waves of a CTA meet only where the K/V slots change hands.
     if (sc->first) {
       issue_q_stage(bh, qb);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    asm volatile("s_barrier" ::: "memory");  // every wave's share of the stage has landed
     const int rr = wave * kQRowsPerTile + r;
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds)
       qf[ds] = *reinterpret_cast<const bf16x8*>(qstage + rr * 256 + 16 * ((2 * ds + g) ^ (rr & 15)));
-    // The stage is read and every wave is done with the previous item's blocks.
-    lds_reads_done_barrier();
+    // The wave's stage rows are read before its next prefetch refills them.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   } else {
     int qr = q_row0 + r;
     qr = qr < p.Sq ? qr : p.Sq - 1;
@@ -448,9 +451,12 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // The head's blocks stay in the slots across its q-blocks; then the next
       // item's Q goes out (8 DMAs per wave), which the block wait leaves in
       // flight.
-      const bool kv_new = sc->resident != bh;
-      if (kv_new)
+      const bool kv_new = sc->resident != bh;  // CTA-uniform
+      if (kv_new) {
+        // Every wave is done with the previous head's blocks.
+        lds_reads_done_barrier();
         for (int j = 0; j < nblk; ++j) issue_kv(blk_of(j), j);
+      }
       const bool prefetch = sc->next_bh >= 0;
       if (prefetch) issue_q_stage(sc->next_bh, sc->next_qb);
       if (kv_new) {
@@ -478,7 +484,10 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     mask(sA, blk_of(0));
     row_m = fmaxf(block_max(sA, 0), kNegFltMax);
 
-    auto step = [&](int i, f32x16 (&scur)[2], f32x16 (&snext)[2]) {
+    // LAST: the tile's last step, with no next block to score (its QK MFMAs
+    // and K fragment reads are left out).
+    auto step = [&](int i, f32x16 (&scur)[2], f32x16 (&snext)[2], auto last) {
+      constexpr bool LAST = decltype(last)::value;
       // Lite: the list entries of blocks i and i+3 are read before the barrier,
       // whose lgkmcnt(0) covers their latency.
       int kb_raw = 0, kb3_raw = 0;
@@ -589,13 +598,18 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // wins issue slots over its SIMD partner when both are ready (measured
       // -0.7% to -2.8% at the headline shape).
       __builtin_amdgcn_s_setprio(1);
-      snext[0] = f32x16{};
-      snext[1] = f32x16{};
-      bf16x8 kf0 = kfrag(0, 0), kf1 = kfrag(1, 0);
+      bf16x8 kf0, kf1;
+      if constexpr (!LAST) {
+        snext[0] = f32x16{};
+        snext[1] = f32x16{};
+        kf0 = kfrag(0, 0);
+        kf1 = kfrag(1, 0);
+      }
       // The previous block's last 4 PV MFMAs (operands in registers since
       // before the barrier) cover the latency of these first K reads:
-      // 1.435 -> 1.411 ms at the headline shape (RTNA, one box).
-      if (!LITE || tail_on) {
+      // 1.435 -> 1.411 ms at the headline shape (RTNA, one box). The first
+      // step has no previous block.
+      if (i > 0 && (!LITE || tail_on)) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
@@ -609,7 +623,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
 #pragma unroll
       for (int ds = 0; ds < 8; ++ds) {
         bf16x8 nk0, nk1;
-        if (ds + 1 < 8) {
+        if (!LAST && ds + 1 < 8) {
           nk0 = kfrag(0, ds + 1);
           nk1 = kfrag(1, ds + 1);
         }
@@ -617,7 +631,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
 #pragma unroll
           for (int k = 0; k < 4; ++k) vb[k] = vfrag_n(k);
         }
-        snext[0] = mfma32(kf0, qf[ds], snext[0]);
+        if constexpr (!LAST) snext[0] = mfma32(kf0, qf[ds], snext[0]);
         sm_pair(0, ds, neg_m0);
         if constexpr (LITE) {
           const int t = ds >> 2, e0 = 4 * (ds & 3);
@@ -625,9 +639,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
           vmx = fmaxf(fmaxf(vmx, scur[t][e0 + 2]), scur[t][e0 + 3]);
         }
         if (ds & 1) dma3_step(ds >> 1);
-        snext[1] = mfma32(kf1, qf[ds], snext[1]);
+        if constexpr (!LAST) snext[1] = mfma32(kf1, qf[ds], snext[1]);
         if (ds & 1) sm_pair(1, ds >> 1, neg_m0);
-        if (ds + 1 < 8) {
+        if (!LAST && ds + 1 < 8) {
           kf0 = nk0;
           kf1 = nk1;
         }
@@ -705,10 +719,20 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         if constexpr (LITE) run_mx = fmaxf(run_mx, xor32_max(bmh));
       }
     };
-    for (int i = 0; i < nblk; i += 2) {
-      step(i, sA, sB);
-      if (i + 1 < nblk) step(i + 1, sB, sA);
+    int i = 0;
+    if constexpr (!SHORT) {  // short KV: at most two blocks
+      for (; i + 2 < nblk; i += 2) {
+        step(i, sA, sB, std::false_type{});
+        step(i + 1, sB, sA, std::false_type{});
+      }
     }
+    if (i + 1 < nblk) {
+      step(i, sA, sB, std::false_type{});
+      ++i;
+      sA[0] = sB[0];  // the last block's scores, where the last step reads them
+      sA[1] = sB[1];
+    }
+    step(i, sA, sB, std::true_type{});
     // The last block's deferred PV MFMAs.
     if (!LITE || tail_on) {
 #pragma unroll
@@ -834,13 +858,34 @@ __global__ __launch_bounds__(kThreads, 1) void attn_short_kernel(Params p, int p
   }
 }
 
-// LiteAttention forward: one CTA per (b, h, q-block); grid slot i runs CTA
-// order[i] (LPT order) or, without an order, the XCD-grouped dense mapping.
+// Grid slot -> position in the LPT order. Slot s runs on XCD s % 8, and each
+// XCD starts its slots in order, one per CU (32 at a time). Round r of the
+// grid (slots 256r .. 256r + 255) takes order positions [256r, 256r + 256):
+// XCD x takes the contiguous run x of 32 positions (run 7 - x in odd rounds,
+// so no XCD always draws the heaviest run of a round). CTAs that run together
+// on one XCD are neighbours in the order -- the q-blocks of one head when
+// their kept counts share a bucket, every q-block of the head in a
+// compute-all step -- and read the same K/V through that XCD's L2. A partial
+// last round is dealt as the dense mapping deals a grid.
+constexpr int kCusPerXcd = 32;
+__device__ __forceinline__ int lpt_position(int s, int total) {
+  constexpr int kRound = kNumXcds * kCusPerXcd;
+  const int base = s - s % kRound;
+  const int idx = s - base;
+  if (total - base < kRound) return base + xcd_remap(idx, total - base);
+  const int x = idx % kNumXcds;
+  const int run = ((base / kRound) & 1) ? kNumXcds - 1 - x : x;
+  return base + run * kCusPerXcd + idx / kNumXcds;
+}
+
+// LiteAttention forward: one CTA per (b, h, q-block); grid slot s runs CTA
+// order[lpt_position(s)] (LPT order) or, without an order, the XCD-grouped
+// dense mapping.
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 1) void attn_lite_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsLiteBytes];
   const int total = p.nqb * p.B * p.H;
-  const int w = p.order ? p.order[blockIdx.x] : xcd_remap(blockIdx.x, total);
+  const int w = p.order ? p.order[lpt_position(blockIdx.x, total)] : xcd_remap(blockIdx.x, total);
   if (w < 0 || w >= total) return;
   run_tile<MODE, true>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds);
 }
