@@ -546,7 +546,13 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         const int ss = pi >> 2, e2 = pi & 3;
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(scur[t][8 * ss + 2 * e2], c, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(scur[t][8 * ss + 2 * e2 + 1], c, neg_m));
-        lpart[t * 2 + ss] += p0 + p1;
+        // The first pair starts the half's sum (0 + x is not folded: -0 + 0
+        // is +0; a sum of p is never -0, so the result is the same).
+        if (e2 == 0) {
+          lpart[t * 2 + ss] = p0 + p1;
+        } else {
+          lpart[t * 2 + ss] += p0 + p1;
+        }
         w[t][ss][e2] = pack2_bf16<MODE>(p0, p1);
       };
       auto pack_pf = [&](int t) {
