@@ -94,6 +94,7 @@ static_assert(kLdsShortBytes <= 160 * 1024, "short-KV LDS fits a CU");
 
 // Item state of a persistent short-KV CTA across run_tile calls.
 struct ShortCtx {
+  int item;      // items this CTA has run
   int resident;  // (b, h) whose K / V_t blocks are in the slots, or -1
   int next_bh;   // the next item's (b, h) and q-block, whose Q is prefetched
   int next_qb;   //   into the stage during this item (next_bh < 0: none)
@@ -223,6 +224,12 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31;  // query column owned by this lane
   const int g = lane >> 5;  // lane half
+  // Short KV (no barrier between items): the two waves of a SIMD (w and
+  // w + 4) take turns at the higher priority level item by item; otherwise
+  // the older wave wins every tie and the younger one falls behind, and the
+  // CTA ends with the younger waves running alone.
+  bool boost = false;
+  if constexpr (SHORT) boost = ((sc->item + (wave >> 2)) & 1) != 0;
 
   const int b = bh / p.H, h = bh % p.H;
   const long long row_stride = p.bshd ? (long long)p.H * kD : kD;
@@ -603,7 +610,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // Raised wave priority over the QK + softmax phase: the wave in this phase
       // wins issue slots over its SIMD partner when both are ready (measured
       // -0.7% to -2.8% at the headline shape).
-      __builtin_amdgcn_s_setprio(1);
+      if (boost) {
+        __builtin_amdgcn_s_setprio(2);
+      } else {
+        __builtin_amdgcn_s_setprio(1);
+      }
       bf16x8 kf0, kf1;
       if constexpr (!LAST) {
         snext[0] = f32x16{};
@@ -654,7 +665,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         sched_fence();
       }
       pack_pf(0);
-      __builtin_amdgcn_s_setprio(0);
+      if (boost) {
+        __builtin_amdgcn_s_setprio(1);
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
       // Lite vote, decided before any PV, rebase or sum of this block (per-wave
       // soft skip, reference :983-1001 and :891-898): the wave keeps the block
       // if some valid row's block max came within `threshold` of the row's
@@ -854,13 +869,14 @@ __global__ __launch_bounds__(kThreads, 1) void attn_short_kernel(Params p, int p
   const int total = p.nqb * p.B * p.H;
   const int w0 = blockIdx.x * per_cta;
   const int w1 = w0 + per_cta < total ? w0 + per_cta : total;
-  ShortCtx sc{-1, -1, 0, true};
+  ShortCtx sc{0, -1, -1, 0, true};
   for (int w = w0; w < w1; ++w) {
     const int wn = w + 1 < w1 ? w + 1 : -1;
     sc.next_bh = wn >= 0 ? wn / p.nqb : -1;
     sc.next_qb = wn >= 0 ? wn % p.nqb : 0;
     run_tile<MODE, false, true>(p, w / p.nqb, w % p.nqb, 0, p.nkb, -1, lds, &sc);
     sc.first = false;
+    ++sc.item;
   }
 }
 
