@@ -146,6 +146,37 @@ def test_lite_lpt_matches_plain_bitexact(monkeypatch):
     assert torch.equal(a1.read_list, a2.read_list)
 
 
+def test_lite_lpt_full_rounds_match_plain_bitexact(monkeypatch):
+    """800 CTAs (1 x 25 heads x 32 q-tiles): three full rounds of 256 grid
+    slots, whose LPT positions are dealt to the XCDs in runs of 32 (reversed
+    in odd rounds), and a partial fourth; four steps on inputs whose heads
+    keep different numbers of blocks, so the order is not the plain one."""
+    Bf, Hf, Sf = 1, 25, 8192
+    g = torch.Generator().manual_seed(60)
+    q, k, v = (torch.randn(Bf, Sf, Hf, 128, generator=g) for _ in range(3))
+    scale = torch.full((Hf, Sf), 0.05)
+    for h in range(Hf):  # head h: the first 4h + 1 K-blocks hot, the rest cold
+        scale[h, : (4 * h + 1) * 64] = 2.0
+    k = k * scale.t().view(1, Sf, Hf, 1)
+    q, k, v = (t.to(torch.bfloat16).to(DEV) for t in (q, k, v))
+    outs, lists = [], []
+    for plain in (False, True):
+        if plain:
+            monkeypatch.setenv("MOONMATH_LITE_PLAIN", "1")
+        else:
+            monkeypatch.delenv("MOONMATH_LITE_PLAIN", raising=False)
+        attn = ma.LiteAttention(threshold=-3.0, round_mode="rtne", layout="bshd")
+        for _ in range(4):
+            out = attn(q, k, v)
+        torch.cuda.synchronize()
+        outs.append(out)
+        lists.append(attn.read_list.clone())
+    kept = [ol.kept_count(r, Sf // 64) for r in lists[0].cpu().numpy().reshape(-1, Sf // 64 + 2)]
+    assert len(set(kept)) > 8, "the order should not be trivial"
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), "LPT order changed the output"
+    assert torch.equal(lists[0], lists[1])
+
+
 def test_lite_must_do_all_equals_compute_all():
     q, k, v = _peaked()
     ktiles = S // 64
