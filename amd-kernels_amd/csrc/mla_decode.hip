@@ -588,19 +588,22 @@ __global__ __launch_bounds__(kThreads, 1) void mla_decode_kernel(Params p) {
   }
 }
 
-// Merge of one 4-dim slice of one query row over its request's parts:
+// Merge of NU 4-dim slices of one query row over its request's parts:
 // M = max_p m_p, w_p = 2^(m_p - M), out = sum w_p O_p * kv_scale / sum w_p l_p,
-// parts in order. o_at(j) / ml_at(j): part j's 16-byte O slice and (m, l) pair.
-// The (m, l) pairs and O slices of up to kBatch parts are loaded together, so a
-// request of up to kBatch parts costs one round of memory latency.
-template <class OAt, class MlAt>
-__device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_at, MlAt ml_at) {
+// parts in order. o_at(j, u): part j's 16-byte O slice u; ml_at(j): part j's
+// (m, l) pair (shared by the slices: one row). The (m, l) pairs and O slices
+// of up to kBatch parts are loaded together, so a request of up to kBatch
+// parts costs one round of memory latency.
+template <int NU, class OAt, class MlAt>
+__device__ __forceinline__ void merge_slices(int nparts, float kv_scale, OAt o_at, MlAt ml_at, u32x2 (&out)[NU]) {
   constexpr int kBatch = 8;
   float M = -__builtin_inff();
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
   float mb[kBatch], lb[kBatch];
-  f32x4 ob[kBatch];
+  f32x4 ob[kBatch][NU];
   // Parts past the request's last are not loaded (uniform across the CTA: a
   // CTA's cells belong to one request).
   auto load_batch = [&](int j0) {
@@ -610,11 +613,13 @@ __device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_a
         const float2 m_l = *reinterpret_cast<const float2*>(ml_at(j0 + k));
         mb[k] = m_l.x;
         lb[k] = m_l.y;
-        ob[k] = *reinterpret_cast<const f32x4*>(o_at(j0 + k));
+#pragma unroll
+        for (int u = 0; u < NU; ++u) ob[k][u] = *reinterpret_cast<const f32x4*>(o_at(j0 + k, u));
       } else {
         mb[k] = -__builtin_inff();
         lb[k] = 0.f;
-        ob[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < NU; ++u) ob[k][u] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
   };
@@ -625,10 +630,13 @@ __device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_a
         const float diff = mb[k] - M;  // integer-valued or -inf, <= 0
         const float wt =
             (mb[k] == -__builtin_inff()) ? 0.f : ((diff >= -126.f) ? __builtin_ldexpf(1.0f, (int)diff) : 0.f);
-        acc[0] = __builtin_fmaf(wt, ob[k][0], acc[0]);
-        acc[1] = __builtin_fmaf(wt, ob[k][1], acc[1]);
-        acc[2] = __builtin_fmaf(wt, ob[k][2], acc[2]);
-        acc[3] = __builtin_fmaf(wt, ob[k][3], acc[3]);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          acc[u][0] = __builtin_fmaf(wt, ob[k][u][0], acc[u][0]);
+          acc[u][1] = __builtin_fmaf(wt, ob[k][u][1], acc[u][1]);
+          acc[u][2] = __builtin_fmaf(wt, ob[k][u][2], acc[u][2]);
+          acc[u][3] = __builtin_fmaf(wt, ob[k][u][3], acc[u][3]);
+        }
         L = __builtin_fmaf(wt, lb[k], L);
       }
     }
@@ -652,10 +660,18 @@ __device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_a
     }
   }
   const float inv = (L == 0.f) ? 0.f : kv_scale * __builtin_amdgcn_rcpf(L);
-  u32x2 o;
-  o[0] = pack2_bf16_canon<kRTNE>(acc[0] * inv, acc[1] * inv);
-  o[1] = pack2_bf16_canon<kRTNE>(acc[2] * inv, acc[3] * inv);
-  return o;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    out[u][0] = pack2_bf16_canon<kRTNE>(acc[u][0] * inv, acc[u][1] * inv);
+    out[u][1] = pack2_bf16_canon<kRTNE>(acc[u][2] * inv, acc[u][3] * inv);
+  }
+}
+
+template <class OAt, class MlAt>
+__device__ __forceinline__ u32x2 merge_slice(int nparts, float kv_scale, OAt o_at, MlAt ml_at) {
+  u32x2 o[1];
+  merge_slices<1>(nparts, kv_scale, [&](int j, int) { return o_at(j); }, ml_at, o);
+  return o[0];
 }
 
 __device__ __forceinline__ int merge_out_row(const Params& p, int b) {
@@ -693,12 +709,17 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
 // from each part, 16 contiguous bytes per thread, and writes the rows' 256-byte
 // output spans through LDS.
 constexpr int kMergeFragThreads = 1024;
+// One CTA = one request's 32-row tile of the 128-row kernel's records, output
+// dims 256 wp .. 256 wp + 255 (record fragments of waves 2 wp and 2 wp + 1):
+// each thread merges the same 16-byte unit of both waves' fragments, so the
+// grid (B x 2 x row tiles) is one round of resident CTAs with two slices'
+// loads in flight per thread.
 __global__ __launch_bounds__(kMergeFragThreads) void mla_merge_frag_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[32][128];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[32][256];
   const int nrt = p.rec_rows / 32;
-  const int b = blockIdx.x / (4 * nrt);
-  const int k = blockIdx.x % (4 * nrt);  // w * nrt + rt
-  const int w = k / nrt, rt = k % nrt;
+  const int b = blockIdx.x / (2 * nrt);
+  const int kk = blockIdx.x % (2 * nrt);  // wp * nrt + rt
+  const int wp = kk / nrt, rt = kk % nrt;
   const int tid = threadIdx.x;
   const int lane = tid & 63, i4 = (tid >> 6) & 3, j = tid >> 8;
   const int n = lane & 31, g = lane >> 5;
@@ -708,22 +729,25 @@ __global__ __launch_bounds__(kMergeFragThreads) void mla_merge_frag_kernel(Param
   if (nparts <= 1) return;  // uniform: the decode kernel wrote this request's output
   const int row = 32 * rt + n;
   const int mrow = row < p.qrows ? row : p.qrows - 1;  // padding rows read a valid (m, l)
-  const size_t f = ((size_t)(k * 4 + j) * 4 + i4) * 64 + lane;  // 16-byte unit in the record
+  // 16-byte unit of wave w's fragment k = w * nrt + rt in the record.
+  const size_t f0 = ((size_t)((2 * wp * nrt + rt) * 4 + j) * 4 + i4) * 64 + lane;
+  const size_t f1 = f0 + (size_t)nrt * 4 * 4 * 64;  // wave 2 wp + 1
   const float* ml = ws_ml(p);
-  const u32x2 o = merge_slice(
-      nparts, p.kv_scale, [&](int jj) { return ws_rec_o(p, (size_t)rec0 + jj) + f * 4; },
-      [&](int jj) { return ml + (((size_t)rec0 + jj) * p.qrows + mrow) * 2; });
-  *reinterpret_cast<u32x2*>(&tile[n][32 * j + 8 * i4 + 4 * g]) = o;
+  u32x2 o[2];
+  merge_slices<2>(
+      nparts, p.kv_scale,
+      [&](int jj, int u) { return ws_rec_o(p, (size_t)rec0 + jj) + (u ? f1 : f0) * 4; },
+      [&](int jj) { return ml + (((size_t)rec0 + jj) * p.qrows + mrow) * 2; }, o);
+  *reinterpret_cast<u32x2*>(&tile[n][32 * j + 8 * i4 + 4 * g]) = o[0];
+  *reinterpret_cast<u32x2*>(&tile[n][128 + 32 * j + 8 * i4 + 4 * g]) = o[1];
   __syncthreads();
-  // 32 rows x 256 B: thread t < 512 stores 16 B of row t / 16.
-  if (tid < 512) {
-    const int r = tid >> 4, c = tid & 15;
-    const int orow = 32 * rt + r;
-    if (orow < p.qrows) {
-      const int qb = merge_out_row(p, b);
-      *reinterpret_cast<u32x4*>(p.o_lat + ((long long)qb * p.qrows + orow) * kLat + 128 * w + 8 * c) =
-          *reinterpret_cast<const u32x4*>(&tile[r][8 * c]);
-    }
+  // 32 rows x 512 B: thread t stores 16 B of row t / 32.
+  const int r = tid >> 5, c = tid & 31;
+  const int orow = 32 * rt + r;
+  if (orow < p.qrows) {
+    const int qb = merge_out_row(p, b);
+    *reinterpret_cast<u32x4*>(p.o_lat + ((long long)qb * p.qrows + orow) * kLat + 256 * wp + 8 * c) =
+        *reinterpret_cast<const u32x4*>(&tile[r][8 * c]);
   }
 }
 
@@ -921,7 +945,7 @@ int launch(const void* q_lat, const void* q_pe, const void* kv, void* o_lat, con
   else
     hipLaunchKernelGGL(mla_decode_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, st, p);
   if (p.parts > 1 && p.rec_frag) {
-    const long long ctas = (long long)B * 4 * (p.rec_rows / 32);
+    const long long ctas = (long long)B * 2 * (p.rec_rows / 32);
     hipLaunchKernelGGL(mla_merge_frag_kernel, dim3((unsigned)ctas), dim3(kMergeFragThreads), 0, st, p);
   } else if (p.parts > 1) {
     const long long cells = (long long)B * p.qrows * (kLat / 4);
