@@ -392,13 +392,18 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     }
   };
 
-  auto qk = [&](const char* kst, f32x16 (&s)[2]) {
+  // Short KV: a block with at most 32 valid keys leaves its second row tile
+  // out of QK and PV (its scores are masked to -inf, so p = 0, and V_t rows
+  // past Skv are zero: the skipped MFMAs would add exact zeros).
+  auto half_block = [&](int kbk) { return SHORT && kbk * kKvBlock + 32 >= kv_end; };
+  auto qk = [&](const char* kst, f32x16 (&s)[2], bool half) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) s[t] = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
+        if (t == 1 && half) continue;
         const bf16x8 kf = *reinterpret_cast<const bf16x8*>(kst + kfrag_lane + 8192 * t + 512 * ds);
         s[t] = mfma32(kf, qf[ds], s[t]);
       }
@@ -446,6 +451,9 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // Lite: whether the previous block's deferred MFMAs carry a kept block
   // (wave-uniform; a dropped block leaves nothing to add).
   bool tail_on = false;
+  // Short KV: the previous block skipped its second row tile, so its deferred
+  // MFMAs (row tile 1, k-step 1) are skipped too.
+  bool tail_half = false;
   if (nblk > 0) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) oacc[dt] = f32x16{};
@@ -487,7 +495,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
         wait_vmem_barrier<0>();
       }
     }
-    qk(kring, sA);
+    qk(kring, sA, half_block(blk_of(0)));
     mask(sA, blk_of(0));
     row_m = fmaxf(block_max(sA, 0), kNegFltMax);
 
@@ -515,6 +523,8 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       }
       sched_fence();
       const int kb = LITE ? __builtin_amdgcn_readfirstlane(kb_raw & 0x7FFF) : kb_begin + i;
+      const bool half_cur = half_block(kb);
+      const bool half_next = !LAST && half_block(kb + 1);
       // Block kb+3: a full block's 4 DMAs go out one per odd QK step below (all
       // 8 waves issuing theirs back to back after the barrier stall their QK);
       // a partial last block is gathered here.
@@ -626,7 +636,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       // before the barrier) cover the latency of these first K reads:
       // 1.435 -> 1.411 ms at the headline shape (RTNA, one box). The first
       // step has no previous block.
-      if (i > 0 && (!LITE || tail_on)) {
+      if (i > 0 && (!LITE || tail_on) && !tail_half) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
@@ -656,8 +666,10 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
           vmx = fmaxf(fmaxf(vmx, scur[t][e0 + 2]), scur[t][e0 + 3]);
         }
         if (ds & 1) dma3_step(ds >> 1);
-        if constexpr (!LAST) snext[1] = mfma32(kf1, qf[ds], snext[1]);
-        if (ds & 1) sm_pair(1, ds >> 1, neg_m0);
+        if constexpr (!LAST) {
+          if (!half_next) snext[1] = mfma32(kf1, qf[ds], snext[1]);
+        }
+        if ((ds & 1) && !half_cur) sm_pair(1, ds >> 1, neg_m0);
         if (!LAST && ds + 1 < 8) {
           kf0 = nk0;
           kf1 = nk1;
@@ -719,23 +731,26 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
           const bf16x8 a = vb[m & 3];
           vb[m & 3] = vfrag_n(m + 4);
           oacc[dt] = mfma32(a, pf[0][ss], oacc[dt]);
-          if (m < 4) sm_pair(1, 4 + m, neg_m1);
+          if (m < 4 && !half_cur) sm_pair(1, 4 + m, neg_m1);
           sched_fence();
         }
         if (__builtin_amdgcn_ballot_w64(lpart[3] > kGrowLimit) != 0) rebase(2, 4);
         pack_pf(1);
         // PV of row tile 1, k-step 0 (k-step 1 runs after the next barrier,
         // from vtail / ptail).
+        if (!half_cur) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const bf16x8 a = vb[m];
-          vb[m] = vfrag_n(12 + m);
-          oacc[m] = mfma32(a, pf[1][0], oacc[m]);
-          sched_fence();
+          for (int m = 0; m < 4; ++m) {
+            const bf16x8 a = vb[m];
+            vb[m] = vfrag_n(12 + m);
+            oacc[m] = mfma32(a, pf[1][0], oacc[m]);
+            sched_fence();
+          }
+#pragma unroll
+          for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
+          ptail = pf[1][1];
         }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) vtail[m] = vb[m];
-        ptail = pf[1][1];
+        if constexpr (SHORT) tail_half = half_cur;
         row_l += (lpart[0] + lpart[1]) + (lpart[2] + lpart[3]);
         if constexpr (LITE) run_mx = fmaxf(run_mx, xor32_max(bmh));
       }
@@ -755,7 +770,7 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
     }
     step(i, sA, sB, std::true_type{});
     // The last block's deferred PV MFMAs.
-    if (!LITE || tail_on) {
+    if ((!LITE || tail_on) && !tail_half) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) oacc[dt] = mfma32(vtail[dt], ptail, oacc[dt]);
     }
