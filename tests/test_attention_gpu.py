@@ -515,3 +515,43 @@ def test_short_kv_persistent_kernel(B, H, Sq, layout, Skv, mode, monkeypatch):
     assert torch.equal(fast.view(torch.int16), ref_kernel.view(torch.int16)), "short-KV kernel differs"
     heads = [(0, 0), (B - 1, H // 2), (B - 1, H - 1)]
     _check(q, k, v, fast, mode, layout, heads, f"short_kv_{layout}_{B}x{H}_sq{Sq}_skv{Skv}_{mode}")
+
+
+@pytest.mark.parametrize("B,H,Sq,Skv,layout,mode", [(2, 24, 4097, 8192, "bshd", "rtne"),   # tail split + merge
+                                                   (2, 24, 8192, 77, "bshd", "rtz"),      # persistent short-KV
+                                                   (1, 3, 1000, 1000, "bhsd", "rtna")])   # plain, ragged
+def test_forward_graph_capture_replays_match_eager(B, H, Sq, Skv, layout, mode):
+    """`forward` captured in a HIP graph (its V_t and split workspace come from
+    the graph's pool; no host sync or memset inside) and replayed with q, k, v
+    refilled in place, with the program's own eager work between replays:
+    every replay bit-identical to an eager call on the same inputs."""
+    shp = (lambda S: (B, S, H, 128)) if layout == "bshd" else (lambda S: (B, H, S, 128))
+    q = torch.empty(shp(Sq), dtype=torch.bfloat16, device=DEV)
+    k = torch.empty(shp(Skv), dtype=torch.bfloat16, device=DEV)
+    v = torch.empty(shp(Skv), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(q)
+
+    def refill(seed):
+        for i, t in enumerate((q, k, v)):
+            t.copy_(randn_bf16(tuple(t.shape), seed + i))
+
+    refill(70)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        ma.forward(q, k, v, out=out, round_mode=mode, layout=layout)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ma.forward(q, k, v, out=out, round_mode=mode, layout=layout)
+    noise = torch.randn(512, 512, device=DEV)
+    for r in range(3):
+        refill(80 + 10 * r)
+        torch.cuda.synchronize()
+        graph.replay()
+        _ = noise @ noise
+        torch.cuda.synchronize()
+        eager = ma.forward(q, k, v, round_mode=mode, layout=layout)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {r} differs from eager"
