@@ -848,8 +848,11 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
       const int cs = lane & 15;
       const u32x4 v = *reinterpret_cast<const u32x4*>(ost + rr * 256 + 16 * cs);
       const int orow = q_row0 + row;
+      // Non-temporal: the output is written once and not read back by this
+      // launch (8192 x 77: 51.7 -> 49.6 us, 8192 x 512: -1.6%).
       if (orow < p.Sq)
-        *reinterpret_cast<u32x4*>(ohead + (long long)orow * row_stride + 8 * (cs ^ (row & 15))) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(ohead + (long long)orow * row_stride +
+                                                                8 * (cs ^ (row & 15))));
     }
   }
 }
