@@ -701,7 +701,10 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(Params p) {
   const u32x2 o = merge_slice(
       nparts, p.kv_scale, [&](int j) { return ws_rec_o(p, (size_t)rec0 + j) + (size_t)qrow * kLat + d; },
       [&](int j) { return ml + (((size_t)rec0 + j) * p.qrows + qrow) * 2; });
-  *reinterpret_cast<u32x2*>(p.o_lat + ((long long)qb * p.qrows + qrow) * kLat + d) = o;
+  // Non-temporal: written once, read by no later kernel of the call (H=16:
+  // 45.8 -> 44.4 us per call; the same in the decode kernels measured neutral
+  // or slower).
+  __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(p.o_lat + ((long long)qb * p.qrows + qrow) * kLat + d));
 }
 
 // Merge of the 128-row kernel's fragment-order records (see its epilogue):
