@@ -10,6 +10,8 @@
 //    fp8 rows are gathered in 64-token tiles into a shared 4-slot LDS ring;
 //    wave w gathers (9 of the 36 16-byte DMAs per tile) and scores tokens
 //    16w .. 16w+15 of every tile.
+//    The gathers are non-temporal: each token is read by one CTA, once
+//    (44.4 -> 40.8 us per call at the bench's H=16 batch).
 //  * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (16 tokens x 16 rows; all of Q
 //    lives in VGPRs). Softmax in base 2 on the integer grid: each row's max m
 //    is fixed for the whole CTA at the part's first tile, p = exp2(s c - m)
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
             return true;
           }
 #pragma unroll
-          for (int k = 0; k < kCDmaPerSub; ++k) dma16_sbase(base, dma_offv(k), dst + 1024 * k);
+          for (int k = 0; k < kCDmaPerSub; ++k) dma16_sbase_nt(base, dma_offv(k), dst + 1024 * k);
         } else if (fast) {
           const int nv = nvalid > 0 ? nvalid : 1;
 #pragma unroll 1
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
             const int o = dma_off(k);
             const int tg = (o * 7282) >> 22;  // o / 576 for o < 9216
             const int t = tg < nv ? tg : nv - 1;
-            dma16_opaque(base + t * kQK + (o - tg * kQK), dst + 1024 * k);
+            dma16_opaque_nt(base + t * kQK + (o - tg * kQK), dst + 1024 * k);
           }
         } else {
           int tk = tok0 + i;
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
             const int o = dma_off(k);
             const int tg = (o * 7282) >> 22;
             const int row = __shfl(myrow, tg);
-            dma16_opaque(p.kv + (long long)row * kQK + (o - tg * kQK), dst + 1024 * k);
+            dma16_opaque_nt(p.kv + (long long)row * kQK + (o - tg * kQK), dst + 1024 * k);
           }
         }
         return false;
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(kCThreads, 1) void mla_coop_kernel(Params p) {
       auto dma_if = [&](int pending, int k) {
         const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)(pend_dst + 1024 * k);
         const int pu = __builtin_amdgcn_readfirstlane(pending);
-        asm volatile("s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\tglobal_load_lds_dwordx4 %0, %1\n1:" ::"v"(dma_offv(k)),
+        asm volatile("s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\tglobal_load_lds_dwordx4 %0, %1 nt\n1:" ::"v"(dma_offv(k)),
                      "s"(pend_base), "{m0}"(m0v), "s"(pu)
                      : "memory", "scc");
       };

@@ -142,6 +142,16 @@ __device__ __forceinline__ void dma16_sbase(const void* sbase, uint32_t voff, co
   const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
 }
+// Non-temporal forms (cache-policy bit nt) for data each CTA streams once and
+// no other CTA of the launch reads again.
+__device__ __forceinline__ void dma16_opaque_nt(const void* gsrc, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(gsrc), "{m0}"(m0v) : "memory");
+}
+__device__ __forceinline__ void dma16_sbase_nt(const void* sbase, uint32_t voff, const char* lds_dst) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(MM_LDS const char*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
+}
 // Barrier without the implicit vmcnt(0) that __syncthreads() carries, so
 // prefetch DMA stays in flight across it. VMEM_LEFT = loads allowed to remain
 // outstanding (issued after the data the barrier publishes).
