@@ -25,16 +25,22 @@
 //    KV-split factor or on the merge order. The denominator sums unrounded
 //    fp32 p (reference :445-451).
 //  * Output: (O * rcp(l)) rounded per mode with every NaN -> 0x7FFF; l == 0
-//    gives inv = 0 (reference :1114-1117).
+//    gives inv = 0 (reference :1114-1117). Staged through idle LDS so each
+//    store writes whole 256-byte rows, with non-temporal stores.
+//  * At most two KV blocks (short cross-attention): a persistent kernel keeps
+//    a head's K / V_t in LDS across its q-blocks and gathers each item's Q
+//    into a per-wave LDS stage during the previous item.
 //  * KV split: the CTAs of the last, partially filled round of the grid
 //    (the "tail") can be split over KV into G contiguous block ranges; each
 //    part writes unnormalised fp32 (O, m, l) and a merge kernel combines them
 //    (reference :1094-1112, :1239-1279).
 //  * LiteAttention (reference :629-716, :1296-1347, :1497-1542, :1599-1681):
 //    the same kernel walks only the KV blocks its CTA's read list (an int16
-//    run-length row) names, votes per block whether any of its rows came
-//    within `threshold` (log2) of the row's running max, and writes the next
-//    step's list; a planning kernel orders the CTAs heaviest first (LPT).
+//    run-length row) names; each wave votes per block whether any of its 32
+//    rows came within `threshold` (log2) of the row's running max and, if
+//    none did, adds nothing for that block (per-wave soft skip); the CTA
+//    writes the next step's list from the votes, and a planning kernel
+//    orders the CTAs heaviest first (LPT).
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
