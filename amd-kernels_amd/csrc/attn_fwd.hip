@@ -1166,7 +1166,10 @@ constexpr int kSlots = kNumCUs * kMinBlocks;
 
 // Tail KV-split cost model (re-derived from reference
 // csrc/attention_kernel.hip:1349-1393 for 256 CUs and kMinBlocks CTAs per CU).
-constexpr int kMinKvBlocksToSplit = 48;
+// The reference splits from 48 KV blocks; here from 16: with a 48-CTA tail,
+// (2,24,4097) measured 124.7 -> 121 us at 16 blocks and 222.8 -> 207.4 us at
+// 32 with 4 parts, while 8 blocks lost (77 -> 80 us with 2 parts).
+constexpr int kMinKvBlocksToSplit = 16;
 constexpr int kMinBlocksPerPart = 4;
 constexpr int kMergeCostBlocks = 3;
 

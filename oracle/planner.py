@@ -4,24 +4,26 @@ the CU count re-derived for MI355X.
 
 ``slots`` = CUs x CTAs resident per CU (256 x 1 for this build's 256-row CTAs).
 No split when the grid tiles the slots evenly, when the last round is > 95%
-full, or when there are fewer than 48 kv blocks. Otherwise G minimises
+full, or when there are fewer than ``min_kv_blocks`` kv blocks (the reference
+uses 48; this build 16, measured on MI355X). Otherwise G minimises
 ceil(tail*G/slots) * ceil(nkb/G) + 3 over G <= max_parts/tail with
 nkb/G >= 4.
 """
 
-MIN_KV_BLOCKS = 48
+REFERENCE_MIN_KV_BLOCKS = 48
+MIN_KV_BLOCKS = 16
 MIN_BLOCKS_PER_PART = 4
 MERGE_COST = 3
 
 
-def plan_tail(nqb, nbh, nkb, slots, max_parts, enable=True):
+def plan_tail(nqb, nbh, nkb, slots, max_parts, enable=True, min_kv_blocks=MIN_KV_BLOCKS):
     """Returns (prefix_wgs, tail, G, parts)."""
     wgs = nqb * nbh
     none = (wgs, 0, 1, 0)
     if not enable:
         return none
     tail = wgs % slots
-    if tail == 0 or tail > slots * 19 // 20 or nkb < MIN_KV_BLOCKS:
+    if tail == 0 or tail > slots * 19 // 20 or nkb < min_kv_blocks:
         return none
     best_g, best = 1, nkb + MERGE_COST
     g = 2

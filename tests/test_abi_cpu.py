@@ -45,7 +45,8 @@ def test_attention_geometry():
 
 @pytest.mark.parametrize("B,H,S,Skv", [(2, 24, 8192, 8192), (2, 24, 4097, 512), (2, 8, 86016, 86016),
                                        (1, 32, 16384, 16384), (1, 2, 256, 256), (3, 7, 5000, 9000),
-                                       (1, 1, 100000, 100000), (4, 3, 777, 8191)])
+                                       (1, 1, 100000, 100000), (4, 3, 777, 8191), (2, 24, 4097, 1024),
+                                       (2, 24, 4097, 2048), (2, 24, 4097, 960)])
 def test_tail_planner_matches_oracle(B, H, S, Skv):
     geo = _lib.geometry()
     nqb = -(-S // geo["rows_per_cta"])
@@ -59,6 +60,13 @@ def test_tail_planner_splits_the_4097_shape():
     128 kv blocks. G = 16: 768 parts in 3 rounds of 8 blocks, 3 * 8 + 3 = 27,
     beats G = 5 (240 parts, one round of 26 blocks: 29) and no split (131)."""
     assert _lib.plan_tail(2, 24, 4097, 8192) == (768, 48, 16, 768)
+
+
+def test_tail_planner_splits_short_kv_tails():
+    """Below the reference's 48-block threshold: (2,24,4097,2048) has 32 kv
+    blocks, split 5 ways in one round; 960 keys (15 blocks) stay unsplit."""
+    assert _lib.plan_tail(2, 24, 4097, 2048) == (768, 48, 5, 240)
+    assert _lib.plan_tail(2, 24, 4097, 960) == (816, 0, 1, 0)
 
 
 def test_tail_planner_disabled_and_forced():

@@ -449,10 +449,11 @@ def test_forced_tail_split_matches_oracle_and_unsplit(ways, monkeypatch):
     compare_bf16(to_bhsd(bits(split), "bshd"), to_bhsd(bits(plain), "bshd"), scl, 2 * tie)
 
 
-def test_planned_tail_split_fires_and_matches_oracle():
-    """(2,24,4097,8192): 17 q-blocks x 48 heads = 816 CTAs leave a 48-CTA tail
-    that the planner splits (the shape the split is meant for)."""
-    B, H, Sq, Skv = 2, 24, 4097, 8192
+@pytest.mark.parametrize("Skv", [8192, 2048])
+def test_planned_tail_split_fires_and_matches_oracle(Skv):
+    """(2,24,4097,Skv): 17 q-blocks x 48 heads = 816 CTAs leave a 48-CTA tail
+    that the planner splits (16 parts of 8 blocks at 8192 keys, 5 of 7 at 2048)."""
+    B, H, Sq = 2, 24, 4097
     plan = _lib.plan_tail(B, H, Sq, Skv, True, 0)
     assert plan[3] > 0, plan
     q, k, v = _make(B, H, Sq, Skv, "bshd", seed=17)
@@ -460,8 +461,10 @@ def test_planned_tail_split_fires_and_matches_oracle():
     # The tail is the last 48 CTAs in (b*H + h, q-block) order: q-blocks 3..16
     # of head (1,21) and every q-block of heads (1,22) and (1,23).
     rows = np.unique(np.concatenate([_long_rows(Sq, 512, seed=4), np.arange(3840, 4097)]))
-    _check_rows(q, k, v, out, "rtne", "bshd", [(1, 23), (1, 22)], rows, "planned_split_2x24_sq4097_skv8192_tail_rows")
-    _check_rows(q, k, v, out, "rtne", "bshd", [(0, 0)], _long_rows(Sq, 256, seed=2), "planned_split_prefix_rows")
+    _check_rows(q, k, v, out, "rtne", "bshd", [(1, 23), (1, 22)], rows,
+                f"planned_split_2x24_sq4097_skv{Skv}_tail_rows")
+    _check_rows(q, k, v, out, "rtne", "bshd", [(0, 0)], _long_rows(Sq, 256, seed=2),
+                f"planned_split_skv{Skv}_prefix_rows")
 
 
 @pytest.mark.parametrize("mode", ["rtne", "rtna", "rtz"])

@@ -234,6 +234,9 @@ def test_vt_zero_pads_rows_past_skv():
         (40, 13, 192, 512, (520, 0, 1, 0)),    # tail 8 of 512 -> G=1 wins? no: see below
         (40, 16, 192, 512, (512, 128, 4, 512)),
         (500, 1, 192, 512, (500, 0, 1, 0)),    # last round 97.7% full
+        (17, 48, 15, 256, (816, 0, 1, 0)),     # tail 48, 15 kv blocks: below the threshold
+        (17, 48, 16, 256, (768, 48, 4, 192)),  # 16 blocks: 4 parts of 4 (one round) + 3 = 7 < 19
+        (17, 48, 32, 256, (768, 48, 5, 240)),  # 32 blocks: 5 parts of 7 (one round) + 3 = 10 < 35
     ],
 )
 def test_planner_cases(nqb, nbh, nkb, slots, expect):
@@ -253,8 +256,16 @@ def test_planner_hand_case_reference_example():
     (51 < 195). The full search (G <= 608/40 = 15) ends at G=15: 600 parts in
     2 rounds x ceil(192/15) = 13 blocks + 3 = 29, below G=7 (1 x 28 + 3 = 31)
     and G=14 (2 x 14 + 3 = 31)."""
-    got = planner.plan_tail(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608)
+    got = planner.plan_tail(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608,
+                            min_kv_blocks=planner.REFERENCE_MIN_KV_BLOCKS)
     assert got == (304, 40, 15, 600)
+
+
+def test_planner_threshold_reference_vs_this_build():
+    """The reference leaves tails of fewer than 48 kv blocks unsplit; this build
+    splits from 16 (measured on MI355X)."""
+    assert planner.plan_tail(17, 48, 32, 256, 1024, min_kv_blocks=planner.REFERENCE_MIN_KV_BLOCKS) == (816, 0, 1, 0)
+    assert planner.plan_tail(17, 48, 32, 256, 1024) == (768, 48, 5, 240)
 
 
 @pytest.mark.parametrize("out_mode,p_mode", [(ob.RTNE, ob.RTZ), (ob.RTNA, ob.RTZ), (ob.RTZ, ob.RTNE)])
