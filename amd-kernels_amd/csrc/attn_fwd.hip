@@ -1164,14 +1164,24 @@ constexpr int kNumCUs = 256;
 constexpr int kMinBlocks = 1;  // CTAs resident per CU
 constexpr int kSlots = kNumCUs * kMinBlocks;
 
-// Tail KV-split cost model (re-derived from reference
-// csrc/attention_kernel.hip:1349-1393 for 256 CUs and kMinBlocks CTAs per CU).
-// The reference splits from 48 KV blocks; here from 16: with a 48-CTA tail,
-// (2,24,4097) measured 124.7 -> 121 us at 16 blocks and 222.8 -> 207.4 us at
-// 32 with 4 parts, while 8 blocks lost (77 -> 80 us with 2 parts).
+// Tail KV-split cost model, in KV blocks of the last round (after reference
+// csrc/attention_kernel.hip:1349-1393, whose span is rounds x blocks per part
+// + 3 for the merge; re-derived on MI355X with 256 CUs x 1 CTA of 256 rows):
+//   unsplit: nkb + kCtaCostBlocks
+//   G parts: rounds x (ceil(nkb / G) + kCtaCostBlocks) + kMergeCostBlocks
+//            + ceil(tail x G / kPartsPerRecordBlock)
+// kCtaCostBlocks: a CTA's prologue and epilogue (~7 us at ~1.7 us per block);
+// the last term: each part's 133 KB fp32 record is written and read back by
+// the merge (~64 records per block of time). Measured on (2,24,4097) with a
+// 48-CTA tail: Skv 8192 779 us with the reference's choice (16 parts, three
+// rounds) against 752 us with 5 parts (this model's choice), Skv 4096 417 ->
+// 386 us (5 parts), Skv 2048 226 -> 212 us; Skv 512 (8 blocks) loses with any
+// split (77 -> 80 us), hence no split below 16 blocks (the reference: 48).
 constexpr int kMinKvBlocksToSplit = 16;
 constexpr int kMinBlocksPerPart = 4;
 constexpr int kMergeCostBlocks = 3;
+constexpr int kCtaCostBlocks = 4;
+constexpr int kPartsPerRecordBlock = 64;
 
 struct TailPlan {
   int prefix_wgs, tail, split_ways, parts;
@@ -1201,11 +1211,12 @@ TailPlan plan_tail(int nqb, int nbh, int nkb, int slots, bool enable, int force_
   }
   if (tail == 0 || tail > slots * 19 / 20 || nkb < kMinKvBlocksToSplit) return none;
   int G = 1;
-  long long best = (long long)nkb + kMergeCostBlocks;
+  long long best = (long long)nkb + kCtaCostBlocks;
   for (int gw = 2; gw <= kMaxParts / tail && nkb / gw >= kMinBlocksPerPart; ++gw) {
     const long long rounds = ((long long)tail * gw + slots - 1) / slots;
     const long long per_part = (nkb + gw - 1) / gw;
-    const long long span = rounds * per_part + kMergeCostBlocks;
+    const long long records = ((long long)tail * gw + kPartsPerRecordBlock - 1) / kPartsPerRecordBlock;
+    const long long span = rounds * (per_part + kCtaCostBlocks) + kMergeCostBlocks + records;
     if (span < best) {
       best = span;
       G = gw;

@@ -57,15 +57,15 @@ def test_tail_planner_matches_oracle(B, H, S, Skv):
 
 def test_tail_planner_splits_the_4097_shape():
     """(2,24,4097,8192): 17 q-blocks x 48 heads = 816 CTAs, a 48-CTA tail over
-    128 kv blocks. G = 16: 768 parts in 3 rounds of 8 blocks, 3 * 8 + 3 = 27,
-    beats G = 5 (240 parts, one round of 26 blocks: 29) and no split (131)."""
-    assert _lib.plan_tail(2, 24, 4097, 8192) == (768, 48, 16, 768)
+    128 kv blocks. G = 5: 240 parts in one round of 26 blocks,
+    (26 + 4) + 3 + 4 = 37, beats G = 16 (three rounds of 8: 51) and no split (132)."""
+    assert _lib.plan_tail(2, 24, 4097, 8192) == (768, 48, 5, 240)
 
 
 def test_tail_planner_splits_short_kv_tails():
     """Below the reference's 48-block threshold: (2,24,4097,2048) has 32 kv
-    blocks, split 5 ways in one round; 960 keys (15 blocks) stay unsplit."""
-    assert _lib.plan_tail(2, 24, 4097, 2048) == (768, 48, 5, 240)
+    blocks, split 4 ways in one round; 960 keys (15 blocks) stay unsplit."""
+    assert _lib.plan_tail(2, 24, 4097, 2048) == (768, 48, 4, 192)
     assert _lib.plan_tail(2, 24, 4097, 960) == (816, 0, 1, 0)
 
 

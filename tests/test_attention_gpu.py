@@ -452,7 +452,7 @@ def test_forced_tail_split_matches_oracle_and_unsplit(ways, monkeypatch):
 @pytest.mark.parametrize("Skv", [8192, 2048])
 def test_planned_tail_split_fires_and_matches_oracle(Skv):
     """(2,24,4097,Skv): 17 q-blocks x 48 heads = 816 CTAs leave a 48-CTA tail
-    that the planner splits (16 parts of 8 blocks at 8192 keys, 5 of 7 at 2048)."""
+    that the planner splits (5 parts of 26 blocks at 8192 keys, 4 of 8 at 2048)."""
     B, H, Sq = 2, 24, 4097
     plan = _lib.plan_tail(B, H, Sq, Skv, True, 0)
     assert plan[3] > 0, plan

@@ -234,15 +234,12 @@ def test_vt_zero_pads_rows_past_skv():
         (40, 13, 192, 512, (520, 0, 1, 0)),    # tail 8 of 512 -> G=1 wins? no: see below
         (40, 16, 192, 512, (512, 128, 4, 512)),
         (500, 1, 192, 512, (500, 0, 1, 0)),    # last round 97.7% full
-        (17, 48, 15, 256, (816, 0, 1, 0)),     # tail 48, 15 kv blocks: below the threshold
-        (17, 48, 16, 256, (768, 48, 4, 192)),  # 16 blocks: 4 parts of 4 (one round) + 3 = 7 < 19
-        (17, 48, 32, 256, (768, 48, 5, 240)),  # 32 blocks: 5 parts of 7 (one round) + 3 = 10 < 35
     ],
 )
 def test_planner_cases(nqb, nbh, nkb, slots, expect):
-    # (40,16): 640 CTAs, tail 128; G <= 4 keeps one round: G=4 -> 48+3 = 51,
-    # G=8 -> 2 rounds x 24 + 3 = 51 (not better) -> G=4.
-    got = planner.plan_tail(nqb, nbh, nkb, slots, 1024)
+    # The reference's rule. (40,16): 640 CTAs, tail 128; G <= 4 keeps one
+    # round: G=4 -> 48+3 = 51, G=8 -> 2 rounds x 24 + 3 = 51 (not better) -> G=4.
+    got = planner.plan_tail_reference(nqb, nbh, nkb, slots, 1024)
     if (nqb, nbh) == (40, 13):
         # 520 CTAs, tail 8: G up to 64 in one round (8*64=512): span ceil(192/48)=4 at
         # G=48 (nkb/G >= 4 caps G at 48) -> 4+3 = 7.
@@ -256,16 +253,41 @@ def test_planner_hand_case_reference_example():
     (51 < 195). The full search (G <= 608/40 = 15) ends at G=15: 600 parts in
     2 rounds x ceil(192/15) = 13 blocks + 3 = 29, below G=7 (1 x 28 + 3 = 31)
     and G=14 (2 x 14 + 3 = 31)."""
-    got = planner.plan_tail(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608,
-                            min_kv_blocks=planner.REFERENCE_MIN_KV_BLOCKS)
+    got = planner.plan_tail_reference(nqb=344, nbh=1, nkb=192, slots=304, max_parts=608)
     assert got == (304, 40, 15, 600)
 
 
-def test_planner_threshold_reference_vs_this_build():
-    """The reference leaves tails of fewer than 48 kv blocks unsplit; this build
-    splits from 16 (measured on MI355X)."""
-    assert planner.plan_tail(17, 48, 32, 256, 1024, min_kv_blocks=planner.REFERENCE_MIN_KV_BLOCKS) == (816, 0, 1, 0)
-    assert planner.plan_tail(17, 48, 32, 256, 1024) == (768, 48, 5, 240)
+@pytest.mark.parametrize(
+    "nqb,nbh,nkb,slots,expect",
+    [
+        (64, 48, 128, 512, (3072, 0, 1, 0)),   # tiles the slots evenly
+        (500, 1, 192, 512, (500, 0, 1, 0)),    # last round 97.7% full
+        (17, 48, 15, 256, (816, 0, 1, 0)),     # tail 48, 15 kv blocks: below the threshold
+        # 128 blocks, tail 48: G=5 (240 parts, one round) -> (26 + 4) + 3 + 4 = 37;
+        # G=4 -> 36 + 3 + 3 = 42; G=6 (two rounds) -> 2 * 26 + 3 + 5 = 60; G=16
+        # (the reference's choice, three rounds) -> 3 * 12 + 3 + 12 = 51; unsplit 132.
+        (17, 48, 128, 256, (768, 48, 5, 240)),
+        # 32 blocks: G=4 -> (8 + 4) + 3 + 3 = 18 ties G=5 -> (7 + 4) + 3 + 4 = 18; the
+        # first minimum is kept; unsplit 36.
+        (17, 48, 32, 256, (768, 48, 4, 192)),
+        # 16 blocks: G=4 -> (4 + 4) + 3 + 3 = 14 < G=3 -> 16 < G=2 -> 17 < unsplit 20.
+        (17, 48, 16, 256, (768, 48, 4, 192)),
+        # 12 CTAs (a grid below one round), 16 blocks: G=4 -> 8 + 3 + 1 = 12 < 20.
+        (1, 12, 16, 256, (0, 12, 4, 48)),
+    ],
+)
+def test_planner_cases_this_build(nqb, nbh, nkb, slots, expect):
+    assert planner.plan_tail(nqb, nbh, nkb, slots, 1024) == expect
+
+
+def test_planner_this_build_vs_reference():
+    """Where the two rules part: the reference leaves a 32-block tail unsplit
+    and splits a 128-block one 16 ways over three rounds; this build splits
+    both, the latter 5 ways in one round."""
+    assert planner.plan_tail_reference(17, 48, 32, 256, 1024) == (816, 0, 1, 0)
+    assert planner.plan_tail(17, 48, 32, 256, 1024) == (768, 48, 4, 192)
+    assert planner.plan_tail_reference(17, 48, 128, 256, 1024) == (768, 48, 16, 768)
+    assert planner.plan_tail(17, 48, 128, 256, 1024) == (768, 48, 5, 240)
 
 
 @pytest.mark.parametrize("out_mode,p_mode", [(ob.RTNE, ob.RTZ), (ob.RTNA, ob.RTZ), (ob.RTZ, ob.RTNE)])
