@@ -296,6 +296,39 @@ __device__ __forceinline__ void run_tile(const Params& p, int bh, int qb, int kb
   // ---- Q fragments (B operand of S^T = K Q^T), kept in registers --------------
   bf16x8 qf[8];
   const int q_row0 = qb * kRowsPerCta + wave * kQRowsPerTile;
+  // A wave whose 32 query rows all lie past Sq (in the last q-block of a
+  // ragged Sq; dense, unsplit tiles) issues its share of every block's DMAs
+  // and meets every block barrier in the same order as its CTA's other waves,
+  // and computes and stores nothing, so the CTA finishes sooner.
+  if constexpr (!LITE && !SHORT) {
+    if (part < 0 && q_row0 >= p.Sq && kb_end > kb_begin) {
+      const int nb = kb_end - kb_begin;
+      for (int j = 0; j < 3 && j < nb; ++j) {
+        issue_k(kb_begin + j, j);
+        issue_v(kb_begin + j, j);
+      }
+      if (nb > 2) {
+        wait_vmem_barrier<8>();
+      } else if (nb > 1) {
+        wait_vmem_barrier<4>();
+      } else {
+        wait_vmem_barrier<0>();
+      }
+      for (int i = 0; i < nb; ++i) {
+        if (i + 2 < nb) {
+          asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        if (i + 3 < nb) {
+          issue_k(kb_begin + i + 3, (i + 3) % kRing);
+          issue_v(kb_begin + i + 3, (i + 3) % kRing);
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+      return;
+    }
+  }
   // Short KV: Q staged in LDS, row rr's 16-byte chunk cc at
   // rr * 256 + 16 * (cc ^ (rr & 15)); wave w's 8 DMAs fill rows 32w .. 32w+31
   // (instruction i: rows 4i .. 4i+3, lane l -> row 4i + l/16, slot l % 16).
